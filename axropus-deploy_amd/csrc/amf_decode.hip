@@ -1,0 +1,713 @@
+// amf_decode.hip - paged GQA decode attention reading AMF_FMT_INT4_ASYM_G32
+// KV pages with fused dequantization (split-K "flash decoding" + LSE merge).
+//
+// Replaces int4_decode_attention (korith_vllm_ext/int4_decode_attention.py:6-9
+// -> kernels/dispatch.py:117-143: full decompress then matmul/softmax/matmul)
+// and the never-dispatched CUDA kernel it stood for
+// (korith_vllm_ext/kernels/int4_decode_attention.cu:39-177: one CTA per
+// (batch, head), serial online softmax over 128-token tiles).  This kernel
+// adds paging (block tables), GQA and split-K.
+//
+// Work item: one wave per (sequence, KV head, split of split_tokens tokens);
+// grid = (max_splits, num_kv_heads, num_seqs).  The wave walks its split in
+// chunks of 32 tokens (two 16-token pages) and keeps, per query head of the
+// GQA group, a running max m (log2 domain), sum l and an unnormalised output.
+// A second kernel merges the splits.
+//
+// Dequantisation is folded into the dot products.  With K = s*c + z per
+// (token, 32-dim group):
+//   q.k = sum_g [ s_g * sum_{d in g} q_d c_d + z_g * sum_{d in g} q_d ].
+// Codes enter the matrix cores as the exact bf16 value 16 + c (a nibble
+// dropped into the mantissa of 16.0), so sum q_d (16 + c_d) - 16 sum q_d is
+// folded into the per-group constant: s * C + (z - 16 s) * Qsum.
+//
+// MFMA path (v_mfma_f32_16x16x32_bf16, 64 lanes, lane = 16 * hi + lo):
+//  QK^T  computed as S^T[(r,g), t] = sum_k A[(r,g), k] B[k, t] where A holds
+//        q of head r restricted to group g (zero elsewhere: block structure)
+//        and B the 16 tokens' codes; four k-steps of 32 dims.  Lane (t = lo,
+//        j = hi) then owns C[(r = j, g = 0..3), t] and folds the four groups
+//        itself, so every output is useful.
+//  PV    O[(r,g), d] = sum_t W[(r,g), t] (16 + c_{t,d}) with W = p * s_g(t)
+//        split into bf16 hi + lo parts (two MFMAs, ~16-bit weights); the V
+//        pages are stored dim-major in 8x8 tiles, so a lane's B operand (8
+//        tokens of one dim) is one dword of a contiguous 32-byte run.  Only
+//        the row of each output column's own group is used.
+// VALU path: the same data flow with fp32 FMAs (kept for the MFMA-vs-VALU
+// comparison and as a second implementation).
+#include "amf_internal.h"
+#include "amf_kernel_util.h"
+
+namespace {
+
+using namespace amf;
+
+constexpr int kD = 128;          // head_dim
+constexpr int kBS = 16;          // tokens per page
+constexpr int kHBCodes = 1024;   // code bytes of one (page, head) block
+constexpr int kHBParams = 64;    // param words of one (page, head) block
+constexpr int kPartStride = kD + 2;  // split partial: D accumulators, m, l
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -1.0e30f;
+
+typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
+
+struct DecodeArgs {
+  const uint16_t* q;
+  void* out;
+  const uint8_t* kc;
+  const uint32_t* kp;
+  const uint8_t* vc;
+  const uint32_t* vp;
+  int64_t pool_pages;
+  const int32_t* block_tables;
+  int bt_stride;
+  const int32_t* context_lens;
+  int num_q_heads;
+  int num_kv_heads;
+  int split_tokens;
+  int max_splits;
+  int max_context_len;
+  float qk_scale_log2;  // softmax_scale * log2(e)
+  float* ws;
+  int32_t* err_flag;
+};
+
+// ---- lane helpers -----------------------------------------------------------
+
+__device__ __forceinline__ float dpp_ror(float v, int n) {
+  // row_ror:n (rotate within each row of 16 lanes): dpp_ctrl 0x120 + n.
+  int x = __builtin_bit_cast(int, v);
+  switch (n) {
+    case 8: x = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false); break;
+    case 4: x = __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false); break;
+    case 2: x = __builtin_amdgcn_update_dpp(0, x, 0x122, 0xF, 0xF, false); break;
+    default: x = __builtin_amdgcn_update_dpp(0, x, 0x121, 0xF, 0xF, false); break;
+  }
+  return __builtin_bit_cast(float, x);
+}
+
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_ror(v, 8));
+  v = fmaxf(v, dpp_ror(v, 4));
+  v = fmaxf(v, dpp_ror(v, 2));
+  v = fmaxf(v, dpp_ror(v, 1));
+  return v;
+}
+
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_ror(v, 8);
+  v += dpp_ror(v, 4);
+  v += dpp_ror(v, 2);
+  v += dpp_ror(v, 1);
+  return v;
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 8 nibbles of w (element e in bits 4e..4e+3) -> 8 bf16 values 16 + c as an
+// MFMA operand (element 2i in the low half of dword i).  bf16(16 + c) =
+// 0x4180 | c << 3: the low byte is 0x80 | c << 3, the high byte 0x41.
+__device__ __forceinline__ u32x4 nib8_to_bf16_16c(uint32_t w) {
+  const uint32_t lo = ((w << 3) & 0x78787878u) | 0x80808080u;  // byte i: even nibble 2i
+  const uint32_t hi = ((w >> 1) & 0x78787878u) | 0x80808080u;  // byte i: odd nibble 2i+1
+  const uint32_t z01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // lo0 hi0 lo1 hi1
+  const uint32_t z23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
+  const uint32_t k41 = 0x41414141u;
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(k41, z01, 0x04010400u);
+  r[1] = __builtin_amdgcn_perm(k41, z01, 0x04030402u);
+  r[2] = __builtin_amdgcn_perm(k41, z23, 0x04010400u);
+  r[3] = __builtin_amdgcn_perm(k41, z23, 0x04030402u);
+  return r;
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+
+__device__ __forceinline__ float pscale(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float pzero(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// Query element as fp32 (bf16 or fp16 storage).
+template <bool QBF16>
+__device__ __forceinline__ float qval(uint16_t b) {
+  if constexpr (QBF16) return u2f((uint32_t)b << 16);
+  else return (float)__builtin_bit_cast(_Float16, b);
+}
+
+template <bool QBF16>
+__device__ __forceinline__ uint16_t oval(float x) {
+  if constexpr (QBF16) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  } else {
+    keep_f32(x);
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+}
+
+struct SplitRange {
+  int begin, end;  // token range of this split; begin >= end: nothing to do
+};
+
+// Context length of sequence s, clamped to what the block table and the
+// launch (max_context_len, which sized the grid and the workspace) cover.
+__device__ __forceinline__ int clamp_context(const DecodeArgs& a, int s) {
+  int ctx = a.context_lens[s];
+  const int max_tok = min(a.bt_stride * kBS, a.max_context_len);
+  if (ctx > max_tok || ctx < 0) {
+    if (threadIdx.x == 0 && a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_CONTEXT);
+    ctx = ctx < 0 ? 0 : max_tok;
+  }
+  return ctx;
+}
+
+// Physical page of logical page `pi` (which must lie inside the context);
+// out-of-range ids are reported and replaced by page 0 with ok = false.
+__device__ __forceinline__ int64_t page_of(const DecodeArgs& a, const int32_t* bt, int pi,
+                                           bool in_ctx, bool* ok) {
+  if (!in_ctx) {
+    *ok = false;
+    return 0;
+  }
+  const int v = bt[pi];
+  *ok = v >= 0 && (int64_t)v < a.pool_pages;
+  if (!*ok && threadIdx.x == 0 && a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+  return *ok ? (int64_t)v : 0;
+}
+
+// ============================================================== MFMA path ==
+
+template <int R, bool QBF16>
+__global__ __launch_bounds__(64) void int4_decode_mfma_kernel(DecodeArgs a) {
+  constexpr int NT = (R + 3) / 4;  // 16-row tiles of (head, group) pairs
+  const int sp = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+  const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
+  const int ctx = clamp_context(a, s);
+  const int tok_begin = sp * a.split_tokens;
+  if (tok_begin >= ctx) return;
+  const int tok_end = min(ctx, tok_begin + a.split_tokens);
+  const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
+  const int H = a.num_kv_heads;
+  const uint16_t* qh = a.q + ((int64_t)s * a.num_q_heads + (int64_t)h * R) * kD;
+
+  // ---- Q operands (constant for the wave) ----
+  u32x4 qa_hi[NT][4], qa_lo[NT][4];
+  float qsum[NT][4];
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    const int r = 4 * T + (lo >> 2), g = lo & 3;
+    // A operand of k-step st: row (r, g) holds q[r][32 g + 8 st + e] on the
+    // lanes whose k-slice (hi) is group g.
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      u32x4 vh = {0, 0, 0, 0}, vl = {0, 0, 0, 0};
+      if (r < R && g == hi) {
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(qh + r * kD + 32 * hi + 8 * st);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (QBF16) {
+            vh[i] = raw[i];
+          } else {
+            const float x0 = qval<false>((uint16_t)(raw[i] & 0xFFFFu));
+            const float x1 = qval<false>((uint16_t)(raw[i] >> 16));
+            const uint32_t h0 = bf16_bits(x0), h1 = bf16_bits(x1);
+            vh[i] = h0 | (h1 << 16);
+            vl[i] = bf16_bits(x0 - u2f(h0 << 16)) | (bf16_bits(x1 - u2f(h1 << 16)) << 16);
+          }
+        }
+      }
+      qa_hi[T][st] = vh;
+      qa_lo[T][st] = vl;
+    }
+    // Qsum[r][g] = sum of q[r][32 g .. 32 g + 31]: lanes (lo, hi) add 8 of
+    // them, a cross-row sum completes it, then lane (t, j) fetches the four
+    // groups of head 4T + j.
+    float part = 0.0f;
+    if (r < R) {
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(qh + r * kD + 32 * g + 8 * hi);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        part += qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu)) + qval<QBF16>((uint16_t)(raw[i] >> 16));
+    }
+    part += __shfl_xor(part, 16);
+    part += __shfl_xor(part, 32);
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) qsum[T][gi] = __shfl(part, 4 * hi + gi);
+  }
+
+  float m_run[NT], l_run[NT], corr[NT];
+  f32x4 acc[NT][8];
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    m_run[T] = kNegBig;
+    l_run[T] = 0.0f;
+    corr[T] = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[T][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  __shared__ __attribute__((aligned(16))) float p_lds[NT][2][4][16];
+
+  for (int c0 = tok_begin; c0 < tok_end; c0 += 32) {
+    const int pi0 = c0 / kBS;
+    bool pok[2];
+    int64_t pg[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pg[u] = page_of(a, bt, pi0 + u, (pi0 + u) * kBS < tok_end, &pok[u]);
+
+    // ---- loads: K (codes + params) of both pages, V codes + params ----
+    u32x4 kcode[2], kpar[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t hb = pg[u] * H + h;
+      kcode[u] = *reinterpret_cast<const u32x4*>(a.kc + hb * kHBCodes + lo * 64 + hi * 16);
+      kpar[u] = *reinterpret_cast<const u32x4*>(a.kp + hb * kHBParams + lo * 4);
+    }
+    const int vu = hi >> 1, vhalf = hi & 1;
+    const int64_t vhb = pg[vu] * H + h;
+    const u32x4* vcp = reinterpret_cast<const u32x4*>(a.vc + vhb * kHBCodes + 64 * lo + 32 * vhalf);
+    const u32x4 vc0 = vcp[0], vc1 = vcp[1];
+    const u32x4* vpp = reinterpret_cast<const u32x4*>(a.vp + vhb * kHBParams + (lo & 3) * 16 + 8 * vhalf);
+    const u32x4 vp0 = vpp[0], vp1 = vpp[1];
+
+    // ---- QK^T and online softmax ----
+    float x[NT][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      u32x4 kb[4];
+#pragma unroll
+      for (int st = 0; st < 4; ++st) kb[st] = nib8_to_bf16_16c(kcode[u][st]);
+      float ks[4], kz[4];
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        ks[gi] = pscale(kpar[u][gi]);
+        kz[gi] = pzero(kpar[u][gi]) - 16.0f * ks[gi];
+      }
+      const bool valid = pok[u] && (c0 + u * kBS + lo) < tok_end;
+#pragma unroll
+      for (int T = 0; T < NT; ++T) {
+        f32x4 cacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          cacc = mfma_bf16(qa_hi[T][st], kb[st], cacc);
+          if constexpr (!QBF16) cacc = mfma_bf16(qa_lo[T][st], kb[st], cacc);
+        }
+        float sc = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) sc += ks[gi] * cacc[gi] + kz[gi] * qsum[T][gi];
+        x[T][u] = valid ? sc * a.qk_scale_log2 : -__builtin_inff();
+      }
+    }
+
+    float p[NT][2];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const float cm = row_max16(fmaxf(x[T][0], x[T][1]));
+      const float m_new = fmaxf(m_run[T], cm);
+      if (__any(m_new > m_run[T])) {
+        const float alpha = exp2_fast(m_run[T] - m_new);
+        l_run[T] *= alpha;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[T][b] *= alpha;
+        // corr lives in the A layout: lane lo holds head 4T + lo/4.
+        corr[T] *= __shfl(alpha, 16 * (lo >> 2));
+        m_run[T] = m_new;
+      }
+      p[T][0] = exp2_fast(x[T][0] - m_run[T]);
+      p[T][1] = exp2_fast(x[T][1] - m_run[T]);
+      l_run[T] += p[T][0] + p[T][1];
+      p_lds[T][0][hi][lo] = p[T][0];
+      p_lds[T][1][hi][lo] = p[T][1];
+    }
+    __builtin_amdgcn_wave_barrier();
+
+    // ---- PV ----
+    u32x4 vb[8];
+    {
+      const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
+#pragma unroll
+      for (int b = 0; b < 8; ++b) vb[b] = nib8_to_bf16_16c(vw[b]);
+    }
+    const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
+    const bool vpage_ok = pok[vu];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      // A row (r', g) = (4T + lo/4, lo%4), k-slice hi: tokens 8 hi .. 8 hi + 7.
+      const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
+      const float4 pa = pl[0], pb = pl[1];
+      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+      u32x4 ahi, alo;
+      float cs = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool valid = vpage_ok && (c0 + 8 * hi + e) < tok_end;
+        const float sv = pscale(pw[e]);
+        const float w = valid ? pv[e] * sv : 0.0f;
+        const uint32_t wh = bf16_bits(w);
+        const uint32_t wl = bf16_bits(w - u2f(wh << 16));
+        if (e & 1) {
+          ahi[e >> 1] |= wh << 16;
+          alo[e >> 1] |= wl << 16;
+        } else {
+          ahi[e >> 1] = wh;
+          alo[e >> 1] = wl;
+        }
+        const float zp = pzero(pw[e]) - 16.0f * sv;
+        cs += valid ? pv[e] * zp : 0.0f;
+      }
+      corr[T] += cs;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        acc[T][b] = mfma_bf16(ahi, vb[b], acc[T][b]);
+        acc[T][b] = mfma_bf16(alo, vb[b], acc[T][b]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // ---- write the split's partial (unnormalised O, m, l) ----
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    const float l_tot = row_sum16(l_run[T]);
+    float cf = corr[T];
+    cf += __shfl_xor(cf, 16);
+    cf += __shfl_xor(cf, 32);
+    const int gsel = lo >> 2;  // group of dims 8 lo .. 8 lo + 7
+    const float cv = __shfl(cf, 4 * hi + gsel);
+    const int r = 4 * T + hi;
+    if (r < R) {
+      float o[8];
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const f32x4 t = acc[T][b];
+        const float v = gsel == 0 ? t[0] : gsel == 1 ? t[1] : gsel == 2 ? t[2] : t[3];
+        o[b] = v + cv;
+      }
+      float* base = a.ws + (((int64_t)s * a.num_q_heads + (int64_t)h * R + r) * a.max_splits + sp) *
+                               kPartStride;
+      *reinterpret_cast<float4*>(base + 8 * lo) = float4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<float4*>(base + 8 * lo + 4) = float4{o[4], o[5], o[6], o[7]};
+      if (lo == 0) {
+        base[kD] = m_run[T];
+        base[kD + 1] = l_tot;
+      }
+    }
+  }
+}
+
+// ============================================================== VALU path ==
+
+template <int R, bool QBF16>
+__global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
+  static_assert(R <= 4, "VALU path: at most 4 query heads per KV head");
+  const int sp = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+  const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
+  const int ctx = clamp_context(a, s);
+  const int tok_begin = sp * a.split_tokens;
+  if (tok_begin >= ctx) return;
+  const int tok_end = min(ctx, tok_begin + a.split_tokens);
+  const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
+  const int H = a.num_kv_heads;
+  const uint16_t* qh = a.q + ((int64_t)s * a.num_q_heads + (int64_t)h * R) * kD;
+
+  // QK layout: lane (t = lo, j = hi) owns K dims 32 j .. 32 j + 31 (group j).
+  float qr[R][32], qs[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    qs[r] = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(qh + r * kD + 32 * hi + 8 * v);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qr[r][8 * v + 2 * i] = qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu));
+        qr[r][8 * v + 2 * i + 1] = qval<QBF16>((uint16_t)(raw[i] >> 16));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) qs[r] += qr[r][i];
+  }
+
+  float m_run = kNegBig, l_run = 0.0f;      // head hi (rows of the score layout)
+  float accv[R][8], zacc[R];                // PV layout: lane (n = lo, j' = hi)
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    zacc[r] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) accv[r][k] = 0.0f;
+  }
+  __shared__ __attribute__((aligned(16))) float p_lds[2][4][16];
+
+  for (int c0 = tok_begin; c0 < tok_end; c0 += 32) {
+    const int pi0 = c0 / kBS;
+    bool pok[2];
+    int64_t pg[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pg[u] = page_of(a, bt, pi0 + u, (pi0 + u) * kBS < tok_end, &pok[u]);
+
+    float x[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t hb = pg[u] * H + h;
+      const u32x4 kc = *reinterpret_cast<const u32x4*>(a.kc + hb * kHBCodes + lo * 64 + hi * 16);
+      const uint32_t kw = a.kp[hb * kHBParams + lo * 4 + hi];
+      const float ks = pscale(kw), kz = pzero(kw);
+      float c[32];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+        for (int n = 0; n < 8; ++n) c[8 * q4 + n] = (float)__builtin_amdgcn_ubfe(kc[q4], 4 * n, 4);
+      float sr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) d = __builtin_fmaf(qr[r][i], c[i], d);
+        float part = ks * d + kz * qs[r];
+        part += __shfl_xor(part, 16);
+        part += __shfl_xor(part, 32);
+        sr[r] = part;
+      }
+      const float mine = hi == 0 ? sr[0] : hi == 1 ? sr[1] : hi == 2 ? sr[2] : sr[3];
+      const bool valid = pok[u] && (c0 + u * kBS + lo) < tok_end && hi < R;
+      x[u] = valid ? mine * a.qk_scale_log2 : -__builtin_inff();
+    }
+    const float cm = row_max16(fmaxf(x[0], x[1]));
+    const float m_new = fmaxf(m_run, cm);
+    if (__any(m_new > m_run)) {
+      const float alpha = exp2_fast(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float ar = __shfl(alpha, 16 * r);
+        zacc[r] *= ar;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) accv[r][k] *= ar;
+      }
+      m_run = m_new;
+    }
+    const float p0 = exp2_fast(x[0] - m_run), p1 = exp2_fast(x[1] - m_run);
+    l_run += p0 + p1;
+    p_lds[0][hi][lo] = p0;
+    p_lds[1][hi][lo] = p1;
+    __builtin_amdgcn_wave_barrier();
+
+    // PV layout: lane (n = lo, j' = hi): dims 8 n .. 8 n + 7, tokens 8 j' .. 8 j' + 7.
+    const int vu = hi >> 1, vhalf = hi & 1;
+    const int64_t vhb = pg[vu] * H + h;
+    const u32x4* vcp = reinterpret_cast<const u32x4*>(a.vc + vhb * kHBCodes + 64 * lo + 32 * vhalf);
+    const u32x4 vc0 = vcp[0], vc1 = vcp[1];
+    const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
+    const u32x4* vpp =
+        reinterpret_cast<const u32x4*>(a.vp + vhb * kHBParams + (lo >> 2) * 16 + 8 * vhalf);
+    const u32x4 vp0 = vpp[0], vp1 = vpp[1];
+    const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool valid = pok[vu] && (c0 + 8 * hi + e) < tok_end;
+      const float sv = pscale(pw[e]), zv = pzero(pw[e]);
+      float cv[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cv[k] = (float)__builtin_amdgcn_ubfe(vw[k], 4 * e, 4);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float pr = valid ? p_lds[vu][r][8 * vhalf + e] : 0.0f;
+        const float w = pr * sv;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) accv[r][k] = __builtin_fmaf(w, cv[k], accv[r][k]);
+        zacc[r] = valid ? __builtin_fmaf(pr, zv, zacc[r]) : zacc[r];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  const float l_tot = row_sum16(l_run);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float v = accv[r][k] + zacc[r];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      o[k] = v;
+    }
+    const float mr = __shfl(m_run, 16 * r), lr = __shfl(l_tot, 16 * r);
+    if (hi == 0) {
+      float* base = a.ws + (((int64_t)s * a.num_q_heads + (int64_t)h * R + r) * a.max_splits + sp) *
+                               kPartStride;
+      *reinterpret_cast<float4*>(base + 8 * lo) = float4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<float4*>(base + 8 * lo + 4) = float4{o[4], o[5], o[6], o[7]};
+      if (lo == 0) {
+        base[kD] = mr;
+        base[kD + 1] = lr;
+      }
+    }
+  }
+}
+
+// ================================================================ merge ====
+
+// One wave per (query head, sequence): O = sum_i 2^(m_i - M) acc_i / L,
+// written as OUT_DTYPE (an AMF_DTYPE_* tag).
+template <int OUT_DTYPE>
+__global__ __launch_bounds__(64) void int4_decode_merge_kernel(DecodeArgs a) {
+  const int qhd = blockIdx.x, s = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int ctx = clamp_context(a, s);
+  const int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
+  const float* base = a.ws + ((int64_t)s * a.num_q_heads + qhd) * a.max_splits * kPartStride;
+  float M = kNegBig;
+  for (int i = 0; i < n_sp; ++i) M = fmaxf(M, base[(int64_t)i * kPartStride + kD]);
+  float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (int i = 0; i < n_sp; ++i) {
+    const float* p = base + (int64_t)i * kPartStride;
+    const float w = exp2_fast(p[kD] - M);
+    L += w * p[kD + 1];
+    o0 += w * p[2 * lane];
+    o1 += w * p[2 * lane + 1];
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  const int64_t row = ((int64_t)s * a.num_q_heads + qhd) * kD;
+  if constexpr (OUT_DTYPE == AMF_DTYPE_F32) {
+    float* out = static_cast<float*>(a.out) + row;
+    *reinterpret_cast<float2*>(out + 2 * lane) = float2{o0 * inv, o1 * inv};
+  } else {
+    constexpr bool BF = OUT_DTYPE == AMF_DTYPE_BF16;
+    uint16_t* out = static_cast<uint16_t*>(a.out) + row;
+    const uint32_t packed = (uint32_t)oval<BF>(o0 * inv) | ((uint32_t)oval<BF>(o1 * inv) << 16);
+    *reinterpret_cast<uint32_t*>(out + 2 * lane) = packed;
+  }
+}
+
+// Split size: a multiple of 32 tokens chosen so that about kTargetWaves waves
+// of work exist when every sequence is max_context_len long.
+constexpr int64_t kTargetWaves = 8192;
+
+int choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context_len) {
+  const int64_t work = (int64_t)num_seqs * num_kv_heads * (max_context_len > 0 ? max_context_len : 1);
+  int64_t split = (work + kTargetWaves - 1) / kTargetWaves;
+  split = (split + 31) / 32 * 32;
+  if (split < 256) split = 256;
+  if (split > 4096) split = 4096;
+  return (int)split;
+}
+
+}  // namespace
+
+extern "C" int64_t amf_int4_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                                   int32_t num_kv_heads, int32_t head_dim,
+                                                   int32_t max_context_len) {
+  if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim != kD) return 0;
+  const int split = choose_split(num_seqs, num_kv_heads, max_context_len);
+  const int64_t max_splits = (max_context_len + split - 1) / split;
+  return (int64_t)num_seqs * num_q_heads * (max_splits > 0 ? max_splits : 1) * kPartStride *
+         (int64_t)sizeof(float);
+}
+
+extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* out,
+                                          int32_t out_dtype,
+                                          const void* k_codes, const void* k_params,
+                                          const void* v_codes, const void* v_params,
+                                          int64_t pool_pages, const int32_t* block_tables,
+                                          int32_t block_table_stride, const int32_t* context_lens,
+                                          int32_t num_seqs, int32_t num_q_heads,
+                                          int32_t num_kv_heads, int32_t head_dim,
+                                          int32_t block_size, int32_t max_context_len,
+                                          float softmax_scale, void* workspace,
+                                          int64_t workspace_bytes, int32_t algo,
+                                          int32_t* err_flag, void* stream) {
+  const char* who = "amf_int4_paged_decode_attn";
+  if (!q || !out || !k_codes || !k_params || !v_codes || !v_params || !block_tables ||
+      !context_lens)
+    return fail(AMF_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  if (q_dtype != AMF_DTYPE_BF16 && q_dtype != AMF_DTYPE_F16)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: q dtype %d is not bf16/fp16", who, q_dtype);
+  if (out_dtype != AMF_DTYPE_BF16 && out_dtype != AMF_DTYPE_F16 && out_dtype != AMF_DTYPE_F32)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: out dtype %d is not bf16/fp16/fp32", who, out_dtype);
+  if (head_dim != kD || block_size != kBS)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: needs head_dim %d and block_size %d (got %d, %d)", who,
+                kD, kBS, head_dim, block_size);
+  if (num_seqs < 0 || num_seqs > 65535 || num_kv_heads <= 0 || num_kv_heads > 65535 ||
+      num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return fail(AMF_ERR_INVALID_ARG, "%s: bad head counts q=%d kv=%d or num_seqs=%d", who,
+                num_q_heads, num_kv_heads, num_seqs);
+  const int R = num_q_heads / num_kv_heads;
+  if (R != 1 && R != 2 && R != 4 && R != 8)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: GQA group %d not in {1,2,4,8}", who, R);
+  if (pool_pages <= 0 || block_table_stride <= 0 || max_context_len < 0)
+    return fail(AMF_ERR_INVALID_ARG, "%s: bad pool_pages / block_table_stride / max_context_len",
+                who);
+  if ((int64_t)max_context_len > (int64_t)block_table_stride * kBS)
+    return fail(AMF_ERR_INVALID_ARG, "%s: max_context_len %d exceeds the block table (%d pages)",
+                who, max_context_len, block_table_stride);
+  if (algo != AMF_DECODE_AUTO && algo != AMF_DECODE_VALU && algo != AMF_DECODE_MFMA)
+    return fail(AMF_ERR_INVALID_ARG, "%s: bad algo %d", who, algo);
+  if (algo == AMF_DECODE_VALU && R > 4)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: the VALU path handles GQA groups up to 4", who);
+  const int64_t need =
+      amf_int4_decode_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_context_len);
+  if (!workspace || workspace_bytes < need)
+    return fail(AMF_ERR_WORKSPACE, "%s: needs %lld workspace bytes", who, (long long)need);
+  if (num_seqs == 0) return ok();
+
+  DecodeArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.out = out;
+  a.kc = static_cast<const uint8_t*>(k_codes);
+  a.kp = static_cast<const uint32_t*>(k_params);
+  a.vc = static_cast<const uint8_t*>(v_codes);
+  a.vp = static_cast<const uint32_t*>(v_params);
+  a.pool_pages = pool_pages;
+  a.block_tables = block_tables;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.split_tokens = choose_split(num_seqs, num_kv_heads, max_context_len);
+  a.max_context_len = max_context_len;
+  const int max_splits = (max_context_len + a.split_tokens - 1) / a.split_tokens;
+  a.max_splits = max_splits > 0 ? max_splits : 1;
+  const float scale = softmax_scale > 0.0f ? softmax_scale : 1.0f / sqrtf((float)head_dim);
+  a.qk_scale_log2 = scale * kLog2e;
+  a.ws = static_cast<float*>(workspace);
+  a.err_flag = err_flag;
+
+  hipStream_t st = as_stream(stream);
+  const bool bf16 = q_dtype == AMF_DTYPE_BF16;
+  if (max_splits > 0) {
+    dim3 grid((unsigned)max_splits, (unsigned)num_kv_heads, (unsigned)num_seqs);
+    const bool valu = algo == AMF_DECODE_VALU;
+#define AMF_LAUNCH(K, RR, B) K<RR, B><<<grid, 64, 0, st>>>(a)
+#define AMF_LAUNCH_B(K, RR) \
+  if (bf16) AMF_LAUNCH(K, RR, true); else AMF_LAUNCH(K, RR, false)
+    if (valu) {
+      if (R == 1) { AMF_LAUNCH_B(int4_decode_valu_kernel, 1); }
+      else if (R == 2) { AMF_LAUNCH_B(int4_decode_valu_kernel, 2); }
+      else { AMF_LAUNCH_B(int4_decode_valu_kernel, 4); }
+    } else {
+      if (R == 1) { AMF_LAUNCH_B(int4_decode_mfma_kernel, 1); }
+      else if (R == 2) { AMF_LAUNCH_B(int4_decode_mfma_kernel, 2); }
+      else if (R == 4) { AMF_LAUNCH_B(int4_decode_mfma_kernel, 4); }
+      else { AMF_LAUNCH_B(int4_decode_mfma_kernel, 8); }
+    }
+#undef AMF_LAUNCH_B
+#undef AMF_LAUNCH
+  }
+  dim3 mgrid((unsigned)num_q_heads, (unsigned)num_seqs);
+  if (out_dtype == AMF_DTYPE_BF16)
+    int4_decode_merge_kernel<AMF_DTYPE_BF16><<<mgrid, 64, 0, st>>>(a);
+  else if (out_dtype == AMF_DTYPE_F16)
+    int4_decode_merge_kernel<AMF_DTYPE_F16><<<mgrid, 64, 0, st>>>(a);
+  else
+    int4_decode_merge_kernel<AMF_DTYPE_F32><<<mgrid, 64, 0, st>>>(a);
+  return check_launch(who);
+}

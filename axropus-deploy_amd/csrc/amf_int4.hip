@@ -1,0 +1,701 @@
+// amf_int4.hip - INT4 codecs of the compressed VRAM pool, fused with the
+// paged gather (save) and paged scatter (restore).
+//
+// Formats (layouts in include/amf_hip.h):
+//  - AMF_FMT_INT4_SYM_BLOCK: INT4PerBlockCodec on a page tensor
+//    (korith_vllm_ext/codecs/amf_codec.py:358-447): the page is the 16-token
+//    axis padded to the codec's 128-token block, so one scale per (plane,
+//    page) over every head.
+//  - AMF_FMT_INT4_SYM: INT4PerChannelCodec (amf_codec.py:305-343): one scale
+//    per head_dim channel over a whole layer, K and V together.
+//  - AMF_FMT_INT4_ASYM_G32: asymmetric 32-dim groups, fp16 (scale, zero).
+// Nibble order of the symmetric formats follows _pack_int4 / _unpack_int4
+// (amf_codec.py:502-539): element 2i in the low nibble, u = q + 8.
+#include "amf_internal.h"
+#include "amf_kernel_util.h"
+
+namespace {
+
+using namespace amf;
+
+constexpr int kThreads = 256;
+constexpr float kSymMax = 7.0f;
+constexpr float kAsymLevels = 15.0f;
+
+// Nibble n (0..7) of a dword, as fp32.
+__device__ __forceinline__ float nib(uint32_t w, int n) {
+  return (float)__builtin_amdgcn_ubfe(w, 4 * n, 4);
+}
+
+// ------------------------------------------------------------ symmetric ----
+
+struct SymGeom {
+  int n_rows;     // block_size * num_heads
+  int head_dim;
+  int cpr_log2;   // log2(head_dim / 32): 32-element chunks per row
+  int pps;        // planes per scale group (per-channel format)
+};
+
+__device__ __forceinline__ int sym_col(const SymGeom& g) { return threadIdx.x & ((1 << g.cpr_log2) - 1); }
+__device__ __forceinline__ int sym_row0(const SymGeom& g) { return threadIdx.x >> g.cpr_log2; }
+__device__ __forceinline__ int sym_rpi(const SymGeom& g) { return kThreads >> g.cpr_log2; }
+
+// 32 cache elements (64 bytes) at `p` -> fp32.
+template <bool BF16>
+__device__ __forceinline__ void load32(const uint8_t* p, float* x) {
+  const u32x4* v = reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) unpack8<BF16>(v[q], x + 8 * q);
+}
+
+template <bool BF16>
+__device__ __forceinline__ void store32(uint8_t* p, const float* x) {
+  u32x4* v = reinterpret_cast<u32x4*>(p);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) __builtin_nontemporal_store(pack8<BF16>(x + 8 * q), v + q);
+}
+
+// CHANNEL = false: INT4_SYM_BLOCK (params: [n_pages] fp16);
+// CHANNEL = true : INT4_SYM       (params: [head_dim] fp16 per layer).
+template <bool BF16, bool CHANNEL>
+__global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
+    const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, SymGeom g, int32_t* err_flag) {
+  const int64_t j = blockIdx.x;
+  const int plane = blockIdx.y;
+  const int64_t dp = block_ids ? (int64_t)block_ids[j] : j;
+  if (dp < 0 || dp >= pool) {
+    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    return;
+  }
+  const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
+  const uint8_t* __restrict__ codes =
+      reinterpret_cast<const uint8_t*>(code_planes[plane]) + j * (page_elems / 2);
+  const _Float16* __restrict__ params = reinterpret_cast<const _Float16*>(param_planes[plane]);
+  uint8_t* __restrict__ out = reinterpret_cast<uint8_t*>(cache_planes[plane]) + dp * cache_stride;
+  const int col = sym_col(g), rpi = sym_rpi(g);
+
+  float s_page = CHANNEL ? 0.0f : (float)params[j];
+  float s_ch[32];
+  if (CHANNEL) {
+#pragma unroll
+    for (int q = 0; q < 32; ++q) s_ch[q] = (float)params[col * 32 + q];
+  }
+  constexpr int U = 4;
+  for (int r = sym_row0(g); r < g.n_rows; r += U * rpi) {
+    u32x4 c[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = r + u * rpi;
+      if (row < g.n_rows)
+        c[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(codes + ((int64_t)row * g.head_dim + col * 32) / 2));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = r + u * rpi;
+      if (row < g.n_rows) {
+        float x[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int n = 0; n < 8; ++n) {
+            const float qv = nib(c[u][q], n) - 8.0f;
+            x[8 * q + n] = qv * (CHANNEL ? s_ch[8 * q + n] : s_page);
+          }
+        store32<BF16>(out + 2 * ((int64_t)row * g.head_dim + col * 32), x);
+      }
+    }
+  }
+}
+
+// INT4_SYM_BLOCK save: page absmax -> scale -> codes; the page stays in
+// registers (R rows of 32 elements per lane).
+template <bool BF16, int R>
+__global__ __launch_bounds__(kThreads) void int4_symblock_quant_gather_kernel(
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
+    const uint64_t* __restrict__ param_planes, SymGeom g, int32_t* err_flag) {
+  const int64_t j = blockIdx.x;
+  const int plane = blockIdx.y;
+  const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
+  if (sp < 0 || sp >= pool) {
+    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    return;
+  }
+  const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
+  const uint8_t* __restrict__ src =
+      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
+  uint8_t* __restrict__ codes = reinterpret_cast<uint8_t*>(code_planes[plane]) + j * (page_elems / 2);
+  _Float16* __restrict__ params = reinterpret_cast<_Float16*>(param_planes[plane]);
+  const int col = sym_col(g), rpi = sym_rpi(g), r0 = sym_row0(g);
+
+  u32x4 v[R][4];
+  float m = 0.0f;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int row = r0 + k * rpi;
+    if (row < g.n_rows) {
+      const u32x4* p =
+          reinterpret_cast<const u32x4*>(src + 2 * ((int64_t)row * g.head_dim + col * 32));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[k][q] = p[q];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float x[8];
+        unpack8<BF16>(v[k][q], x);
+#pragma unroll
+        for (int n = 0; n < 8; ++n) m = fmaxf(m, fabsf(x[n]));
+      }
+    }
+  }
+  m = wave_max_xor(m, 64);
+  __shared__ float s_wmax[kThreads / 64];
+  if ((threadIdx.x & 63) == 0) s_wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float amax = s_wmax[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) amax = fmaxf(amax, s_wmax[w]);
+  // amf_codec.py:392-394: absmax.clamp_min(1e-8) / 7 in fp32.
+  const float scale = fmaxf(amax, 1e-8f) / kSymMax;
+  const float rscale = 1.0f / scale;
+  if (threadIdx.x == 0) params[j] = (_Float16)scale;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int row = r0 + k * rpi;
+    if (row < g.n_rows) {
+      u32x4 c;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float x[8];
+        unpack8<BF16>(v[k][q], x);
+        uint32_t w = 0;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+          float qv = __builtin_rintf(div_rn(x[n], scale, rscale));
+          qv = fminf(fmaxf(qv, -8.0f), 7.0f);
+          w |= (uint32_t)((int)qv + 8) << (4 * n);
+        }
+        c[q] = w;
+      }
+      __builtin_nontemporal_store(
+          c, reinterpret_cast<u32x4*>(codes + ((int64_t)row * g.head_dim + col * 32) / 2));
+    }
+  }
+}
+
+// INT4_SYM save, pass 1: per-channel absmax over a scale group.  Each
+// workgroup folds a strided set of pages into an LDS table, then issues one
+// global atomic max per channel into ws[group][head_dim].
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void int4_channel_absmax_kernel(
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, int64_t n_pages, SymGeom g,
+    uint32_t* ws, int32_t* err_flag) {
+  const int plane = blockIdx.y;
+  __shared__ uint32_t s_max[1024];
+  for (int d = threadIdx.x; d < g.head_dim; d += kThreads) s_max[d] = 0;
+  __syncthreads();
+  const int col = sym_col(g), rpi = sym_rpi(g);
+  float m[32];
+#pragma unroll
+  for (int q = 0; q < 32; ++q) m[q] = 0.0f;
+  for (int64_t j = blockIdx.x; j < n_pages; j += gridDim.x) {
+    const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
+    if (sp < 0 || sp >= pool) {
+      if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+      continue;
+    }
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
+    for (int r = sym_row0(g); r < g.n_rows; r += rpi) {
+      float x[32];
+      load32<BF16>(src + 2 * ((int64_t)r * g.head_dim + col * 32), x);
+#pragma unroll
+      for (int q = 0; q < 32; ++q) m[q] = fmaxf(m[q], fabsf(x[q]));
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 32; ++q) atomicMax(&s_max[col * 32 + q], f2u(m[q]));
+  __syncthreads();
+  for (int d = threadIdx.x; d < g.head_dim; d += kThreads)
+    atomicMax(ws + (int64_t)(plane / g.pps) * g.head_dim + d, s_max[d]);
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void int4_channel_quant_gather_kernel(
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
+    SymGeom g, const uint32_t* __restrict__ ws, int32_t* err_flag) {
+  const int64_t j = blockIdx.x;
+  const int plane = blockIdx.y;
+  const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
+  if (sp < 0 || sp >= pool) {
+    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    return;
+  }
+  const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
+  const uint8_t* __restrict__ src =
+      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
+  uint8_t* __restrict__ codes = reinterpret_cast<uint8_t*>(code_planes[plane]) + j * (page_elems / 2);
+  const int col = sym_col(g), rpi = sym_rpi(g);
+  const uint32_t* lw = ws + (int64_t)(plane / g.pps) * g.head_dim + col * 32;
+  float sc[32], rc[32];
+#pragma unroll
+  for (int q = 0; q < 32; ++q) {
+    sc[q] = fmaxf(u2f(lw[q]), 1e-8f) / kSymMax;  // amf_codec.py:312-313
+    rc[q] = 1.0f / sc[q];
+  }
+  for (int r = sym_row0(g); r < g.n_rows; r += rpi) {
+    float x[32];
+    load32<BF16>(src + 2 * ((int64_t)r * g.head_dim + col * 32), x);
+    u32x4 c;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        float qv = __builtin_rintf(div_rn(x[8 * q + n], sc[8 * q + n], rc[8 * q + n]));
+        qv = fminf(fmaxf(qv, -8.0f), 7.0f);
+        w |= (uint32_t)((int)qv + 8) << (4 * n);
+      }
+      c[q] = w;
+    }
+    __builtin_nontemporal_store(
+        c, reinterpret_cast<u32x4*>(codes + ((int64_t)r * g.head_dim + col * 32) / 2));
+  }
+}
+
+__global__ void int4_channel_finalize_kernel(const uint64_t* __restrict__ param_planes,
+                                             const uint32_t* __restrict__ ws, int n_planes,
+                                             int pps, int head_dim) {
+  const int plane = blockIdx.y;
+  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (plane < n_planes && plane % pps == 0 && d < head_dim) {
+    _Float16* p = reinterpret_cast<_Float16*>(param_planes[plane]);
+    p[d] = (_Float16)(fmaxf(u2f(ws[(int64_t)(plane / pps) * head_dim + d]), 1e-8f) / kSymMax);
+  }
+}
+
+// ----------------------------------------------------------- asymmetric ----
+//
+// Page geometry: block_size 16, G = head_dim / 32 groups.  Per (page, head):
+// K codes [16][D/2], K params [16][G]; V codes tiled dim-major, V params [G][16].
+
+struct AsymGeom {
+  int num_heads;
+  int head_dim;
+  int groups;          // head_dim / 32
+  int hb_code_bytes;   // 16 * head_dim / 2   (one (page, head) code block)
+  int hb_param_words;  // 16 * groups
+};
+
+// Group quantizer: min / max over 32 values, then
+// scale = max(mx - mn, 1e-8) / 15 and q = clamp(rint((x - mn) / scale), 0, 15).
+struct AsymParams {
+  float mn, scale, rscale;
+};
+
+__device__ __forceinline__ AsymParams asym_params(const float* x) {
+  float mn = x[0], mx = x[0];
+#pragma unroll
+  for (int n = 1; n < 32; ++n) {
+    mn = fminf(mn, x[n]);
+    mx = fmaxf(mx, x[n]);
+  }
+  AsymParams p;
+  p.mn = mn;
+  p.scale = fmaxf(mx - mn, 1e-8f) / kAsymLevels;
+  p.rscale = 1.0f / p.scale;
+  return p;
+}
+
+__device__ __forceinline__ uint32_t asym_code(float x, const AsymParams& p) {
+  float q = __builtin_rintf(div_rn(x - p.mn, p.scale, p.rscale));
+  q = fminf(fmaxf(q, 0.0f), kAsymLevels);
+  return (uint32_t)q;
+}
+
+__device__ __forceinline__ uint32_t asym_param_word(const AsymParams& p) {
+  uint32_t s = __builtin_bit_cast(uint16_t, (_Float16)p.scale);
+  uint32_t z = __builtin_bit_cast(uint16_t, (_Float16)p.mn);
+  return s | (z << 16);
+}
+
+__device__ __forceinline__ float param_scale(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float param_zero(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// Restore of one page of one plane; even planes are K, odd planes V (tiled
+// layout).  Items:
+//  K: (head, token, group): 16 code bytes + 1 param word -> 32 outputs of a row
+//  V: (head, 8-dim block, token half): 32 code bytes + 8 param words ->
+//     8 tokens x 8 dims.
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
+    const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, AsymGeom g, int32_t* err_flag) {
+  const int64_t j = blockIdx.x;
+  const int plane = blockIdx.y;
+  const bool is_v = (plane & 1) != 0;
+  const int64_t dp = block_ids ? (int64_t)block_ids[j] : j;
+  if (dp < 0 || dp >= pool) {
+    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    return;
+  }
+  const int H = g.num_heads, D = g.head_dim, G = g.groups;
+  const uint8_t* __restrict__ codes = reinterpret_cast<const uint8_t*>(code_planes[plane]) +
+                                      j * (int64_t)H * g.hb_code_bytes;
+  const uint32_t* __restrict__ params = reinterpret_cast<const uint32_t*>(param_planes[plane]) +
+                                        j * (int64_t)H * g.hb_param_words;
+  uint8_t* __restrict__ out = reinterpret_cast<uint8_t*>(cache_planes[plane]) + dp * cache_stride;
+
+  if (!is_v) {
+    const int n_items = H * 16 * G;
+    for (int it = threadIdx.x; it < n_items; it += kThreads) {
+      const int gi = it % G;
+      const int ht = it / G;  // head * 16 + token
+      const int h = ht >> 4, t = ht & 15;
+      const u32x4 c = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(codes + (int64_t)ht * (D / 2) + 16 * gi));
+      const uint32_t pw = params[ht * G + gi];
+      const float s = param_scale(pw), z = param_zero(pw);
+      float x[32];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int n = 0; n < 8; ++n) x[8 * q + n] = nib(c[q], n) * s + z;
+      store32<BF16>(out + 2 * ((int64_t)(t * H + h) * D + 32 * gi), x);
+    }
+  } else {
+    const int nb = D / 8;
+    const int n_items = H * nb * 2;
+    for (int it = threadIdx.x; it < n_items; it += kThreads) {
+      const int th = it & 1;
+      const int b = (it >> 1) % nb;
+      const int h = (it >> 1) / nb;
+      const u32x4* cp =
+          reinterpret_cast<const u32x4*>(codes + (int64_t)h * g.hb_code_bytes + 64 * b + 32 * th);
+      const u32x4 c0 = __builtin_nontemporal_load(cp);
+      const u32x4 c1 = __builtin_nontemporal_load(cp + 1);
+      const uint32_t w[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+      const u32x4* pp = reinterpret_cast<const u32x4*>(params + h * g.hb_param_words +
+                                                       (b >> 2) * 16 + 8 * th);
+      const u32x4 p0 = pp[0], p1 = pp[1];
+      const uint32_t pw[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float s = param_scale(pw[i]), z = param_zero(pw[i]);
+        float x[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = nib(w[k], i) * s + z;
+        const int t = 8 * th + i;
+        __builtin_nontemporal_store(
+            pack8<BF16>(x),
+            reinterpret_cast<u32x4*>(out + 2 * ((int64_t)(t * H + h) * D + 8 * b)));
+      }
+    }
+  }
+}
+
+// Save of one page of a K plane: items (head, token, group) read 64 cache
+// bytes, write 16 code bytes and one param word.
+template <bool BF16>
+__device__ __forceinline__ void asym_quant_k(const uint8_t* __restrict__ src,
+                                             uint8_t* __restrict__ codes,
+                                             uint32_t* __restrict__ params, const AsymGeom& g) {
+  const int H = g.num_heads, D = g.head_dim, G = g.groups;
+  const int n_items = 16 * H * G;
+  for (int it = threadIdx.x; it < n_items; it += kThreads) {
+    // Items in cache order (token, head, group) so the loads are contiguous.
+    const int gi = it % G;
+    const int th = it / G;  // token * H + head
+    const int t = th / H, h = th % H;
+    float x[32];
+    load32<BF16>(src + 2 * ((int64_t)th * D + 32 * gi), x);
+    const AsymParams p = asym_params(x);
+    u32x4 c;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) w |= asym_code(x[8 * q + n], p) << (4 * n);
+      c[q] = w;
+    }
+    const int ht = h * 16 + t;
+    __builtin_nontemporal_store(c,
+                                reinterpret_cast<u32x4*>(codes + (int64_t)ht * (D / 2) + 16 * gi));
+    params[ht * G + gi] = asym_param_word(p);
+  }
+}
+
+// Save of one page of a V plane.  Groups run along head_dim while the code
+// tiles run along tokens, so the page is staged in LDS: phase 1 computes every
+// group's (mn, scale), phase 2 builds the 8-token x 8-dim tiles.
+constexpr int kAsymLdsBytes = 64 * 1024;
+
+template <bool BF16>
+__device__ __forceinline__ void asym_quant_v(const uint8_t* __restrict__ src,
+                                             uint8_t* __restrict__ codes,
+                                             uint32_t* __restrict__ params, const AsymGeom& g,
+                                             uint8_t* lds) {
+  const int H = g.num_heads, D = g.head_dim, G = g.groups;
+  const int page_bytes = 16 * H * D * 2;
+  // phase 0: page -> LDS (cache layout)
+  for (int o = threadIdx.x * 16; o < page_bytes; o += kThreads * 16)
+    *reinterpret_cast<u32x4*>(lds + o) = *reinterpret_cast<const u32x4*>(src + o);
+  float* s_mn = reinterpret_cast<float*>(lds + page_bytes);          // [H][G][16]
+  float* s_sc = s_mn + 16 * H * G;                                   // [H][G][16]
+  float* s_rc = s_sc + 16 * H * G;                                   // [H][G][16]
+  __syncthreads();
+  const int n_groups = 16 * H * G;
+  for (int it = threadIdx.x; it < n_groups; it += kThreads) {
+    // it = (head, group, token): params are written in V order.
+    const int t = it & 15;
+    const int hg = it >> 4;
+    const int h = hg / G, gi = hg % G;
+    float x[32];
+    const u32x4* v = reinterpret_cast<const u32x4*>(lds + 2 * ((t * H + h) * D + 32 * gi));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) unpack8<BF16>(v[q], x + 8 * q);
+    const AsymParams p = asym_params(x);
+    s_mn[it] = p.mn;
+    s_sc[it] = p.scale;
+    s_rc[it] = p.rscale;
+    params[it] = asym_param_word(p);
+  }
+  __syncthreads();
+  const int nb = D / 8;
+  const int n_items = H * nb * 2;
+  for (int it = threadIdx.x; it < n_items; it += kThreads) {
+    const int th = it & 1;
+    const int b = (it >> 1) % nb;
+    const int h = (it >> 1) / nb;
+    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = 8 * th + i;
+      const int pi = (h * G + (b >> 2)) * 16 + t;
+      AsymParams p;
+      p.mn = s_mn[pi];
+      p.scale = s_sc[pi];
+      p.rscale = s_rc[pi];
+      float x[8];
+      unpack8<BF16>(*reinterpret_cast<const u32x4*>(lds + 2 * ((t * H + h) * D + 8 * b)), x);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) w[k] |= asym_code(x[k], p) << (4 * i);
+    }
+    u32x4* cp = reinterpret_cast<u32x4*>(codes + (int64_t)h * g.hb_code_bytes + 64 * b + 32 * th);
+    __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]}, cp);
+    __builtin_nontemporal_store(u32x4{w[4], w[5], w[6], w[7]}, cp + 1);
+  }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void int4_asym_quant_gather_kernel(
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
+    const uint64_t* __restrict__ param_planes, AsymGeom g, int32_t* err_flag) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int64_t j = blockIdx.x;
+  const int plane = blockIdx.y;
+  const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
+  if (sp < 0 || sp >= pool) {
+    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    return;
+  }
+  const int H = g.num_heads;
+  const uint8_t* __restrict__ src =
+      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
+  uint8_t* __restrict__ codes =
+      reinterpret_cast<uint8_t*>(code_planes[plane]) + j * (int64_t)H * g.hb_code_bytes;
+  uint32_t* __restrict__ params =
+      reinterpret_cast<uint32_t*>(param_planes[plane]) + j * (int64_t)H * g.hb_param_words;
+  if ((plane & 1) == 0)
+    asym_quant_k<BF16>(src, codes, params, g);
+  else
+    asym_quant_v<BF16>(src, codes, params, g, lds);
+}
+
+int check_int4_format(const char* who, int32_t format) {
+  if (format != AMF_FMT_INT4_SYM_BLOCK && format != AMF_FMT_INT4_SYM &&
+      format != AMF_FMT_INT4_ASYM_G32)
+    return fail(AMF_ERR_INVALID_ARG, "%s: format %d is not an INT4 format", who, format);
+  return ok();
+}
+
+int make_sym_geom(const char* who, int32_t block_size, int32_t num_heads, int32_t head_dim,
+                  int32_t pps, SymGeom* g) {
+  const int cpr = head_dim / 32;
+  if (cpr > kThreads || (cpr & (cpr - 1)) != 0)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: head_dim/32 = %d must be a power of two <= %d", who,
+                cpr, kThreads);
+  g->n_rows = block_size * num_heads;
+  g->head_dim = head_dim;
+  g->cpr_log2 = __builtin_ctz(cpr);
+  g->pps = pps > 0 ? pps : 1;
+  return ok();
+}
+
+int make_asym_geom(const char* who, int32_t block_size, int32_t num_heads, int32_t head_dim,
+                   int32_t n_planes, AsymGeom* g, size_t* lds_bytes) {
+  if (block_size != 16)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: INT4_ASYM_G32 needs block_size 16 (got %d)", who,
+                block_size);
+  if (n_planes % 2 != 0)
+    return fail(AMF_ERR_INVALID_ARG, "%s: INT4_ASYM_G32 needs (K, V) plane pairs", who);
+  g->num_heads = num_heads;
+  g->head_dim = head_dim;
+  g->groups = head_dim / 32;
+  g->hb_code_bytes = 16 * head_dim / 2;
+  g->hb_param_words = 16 * g->groups;
+  // LDS of the V save: the page (bf16) + three fp32 tables of 16*H*G entries.
+  *lds_bytes = (size_t)16 * num_heads * head_dim * 2 + (size_t)3 * 4 * 16 * num_heads * g->groups;
+  if (*lds_bytes > (size_t)kAsymLdsBytes)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: page of %d heads x %d dims exceeds the LDS stage", who,
+                num_heads, head_dim);
+  return ok();
+}
+
+}  // namespace
+
+extern "C" int amf_int4_dequant_scatter(int32_t format, const uint64_t* code_planes,
+                                        const uint64_t* param_planes, const uint64_t* cache_planes,
+                                        int64_t cache_page_stride, int32_t cache_dtype,
+                                        const int32_t* block_ids, int64_t pool_pages,
+                                        int32_t n_planes, int64_t n_pages, int32_t block_size,
+                                        int32_t num_heads, int32_t head_dim, int32_t* err_flag,
+                                        void* stream) {
+  const char* who = "amf_int4_dequant_scatter";
+  int rc = check_int4_format(who, format);
+  if (rc) return rc;
+  rc = check_codec_geometry(who, cache_planes, cache_page_stride, cache_dtype, block_ids,
+                            pool_pages, code_planes, param_planes, n_planes, n_pages, block_size,
+                            num_heads, head_dim);
+  if (rc) return rc;
+  const bool bf16 = cache_dtype == AMF_DTYPE_BF16;
+  hipStream_t s = as_stream(stream);
+  dim3 grid((unsigned)n_pages, (unsigned)n_planes);
+  if (format == AMF_FMT_INT4_ASYM_G32) {
+    AsymGeom g;
+    size_t lds;
+    if ((rc = make_asym_geom(who, block_size, num_heads, head_dim, n_planes, &g, &lds))) return rc;
+    if (n_pages == 0) return ok();
+#define AMF_LAUNCH(B)                                                                           \
+  int4_asym_dequant_scatter_kernel<B><<<grid, kThreads, 0, s>>>(                                \
+      code_planes, param_planes, cache_planes, cache_page_stride, block_ids, pool_pages, g, \
+      err_flag)
+    if (bf16) AMF_LAUNCH(true);
+    else AMF_LAUNCH(false);
+#undef AMF_LAUNCH
+    return check_launch(who);
+  }
+  SymGeom g;
+  if ((rc = make_sym_geom(who, block_size, num_heads, head_dim, 1, &g))) return rc;
+  if (n_pages == 0) return ok();
+  const bool ch = format == AMF_FMT_INT4_SYM;
+#define AMF_LAUNCH(B, C)                                                                        \
+  int4_sym_dequant_scatter_kernel<B, C><<<grid, kThreads, 0, s>>>(                              \
+      code_planes, param_planes, cache_planes, cache_page_stride, block_ids, pool_pages, g, \
+      err_flag)
+  if (bf16 && ch) AMF_LAUNCH(true, true);
+  else if (bf16) AMF_LAUNCH(true, false);
+  else if (ch) AMF_LAUNCH(false, true);
+  else AMF_LAUNCH(false, false);
+#undef AMF_LAUNCH
+  return check_launch(who);
+}
+
+extern "C" int amf_int4_quant_gather(int32_t format, const uint64_t* cache_planes,
+                                     int64_t cache_page_stride, int32_t cache_dtype,
+                                     const int32_t* block_ids, int64_t pool_pages,
+                                     const uint64_t* code_planes, const uint64_t* param_planes,
+                                     int32_t n_planes, int32_t planes_per_scale, int64_t n_pages,
+                                     int32_t block_size, int32_t num_heads, int32_t head_dim,
+                                     float* workspace,
+                                     int64_t workspace_bytes, int32_t* err_flag, void* stream) {
+  const char* who = "amf_int4_quant_gather";
+  int rc = check_int4_format(who, format);
+  if (rc) return rc;
+  rc = check_codec_geometry(who, cache_planes, cache_page_stride, cache_dtype, block_ids,
+                            pool_pages, code_planes, param_planes, n_planes, n_pages, block_size,
+                            num_heads, head_dim);
+  if (rc) return rc;
+  const bool bf16 = cache_dtype == AMF_DTYPE_BF16;
+  hipStream_t s = as_stream(stream);
+  dim3 grid((unsigned)n_pages, (unsigned)n_planes);
+  if (format == AMF_FMT_INT4_ASYM_G32) {
+    AsymGeom g;
+    size_t lds;
+    if ((rc = make_asym_geom(who, block_size, num_heads, head_dim, n_planes, &g, &lds))) return rc;
+    if (n_pages == 0) return ok();
+    if (bf16)
+      int4_asym_quant_gather_kernel<true><<<grid, kThreads, lds, s>>>(
+          cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, param_planes, g,
+          err_flag);
+    else
+      int4_asym_quant_gather_kernel<false><<<grid, kThreads, lds, s>>>(
+          cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, param_planes, g,
+          err_flag);
+    return check_launch(who);
+  }
+  if (format == AMF_FMT_INT4_SYM &&
+      (planes_per_scale <= 0 || n_planes % planes_per_scale != 0))
+    return fail(AMF_ERR_INVALID_ARG, "%s: planes_per_scale %d does not divide n_planes %d", who,
+                planes_per_scale, n_planes);
+  SymGeom g;
+  if ((rc = make_sym_geom(who, block_size, num_heads, head_dim, planes_per_scale, &g))) return rc;
+  if (n_pages == 0) return ok();
+  if (format == AMF_FMT_INT4_SYM_BLOCK) {
+    const int rpi = kThreads >> g.cpr_log2;
+    const int rows = (g.n_rows + rpi - 1) / rpi;
+    if (rows > 8)
+      return fail(AMF_ERR_UNSUPPORTED, "%s: page of %d rows exceeds %d", who, g.n_rows, 8 * rpi);
+#define AMF_LAUNCH(B, R)                                                                        \
+  int4_symblock_quant_gather_kernel<B, R><<<grid, kThreads, 0, s>>>(                            \
+      cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, param_planes, g, \
+      err_flag)
+#define AMF_LAUNCH_R(B)                     \
+  if (rows <= 1) AMF_LAUNCH(B, 1);          \
+  else if (rows <= 2) AMF_LAUNCH(B, 2);     \
+  else if (rows <= 4) AMF_LAUNCH(B, 4);     \
+  else AMF_LAUNCH(B, 8)
+    if (bf16) { AMF_LAUNCH_R(true); } else { AMF_LAUNCH_R(false); }
+#undef AMF_LAUNCH_R
+#undef AMF_LAUNCH
+    return check_launch(who);
+  }
+  // AMF_FMT_INT4_SYM: absmax pass, quant pass, fp16 scale finalize.
+  if (head_dim > 1024) return fail(AMF_ERR_UNSUPPORTED, "%s: head_dim > 1024", who);
+  const int64_t need = amf_quant_workspace_bytes(format, n_planes, planes_per_scale, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return fail(AMF_ERR_WORKSPACE, "%s: needs %lld workspace bytes", who, (long long)need);
+  uint32_t* ws = reinterpret_cast<uint32_t*>(workspace);
+  const int64_t n_ws = need / 4;
+  fill_u32_kernel<<<(unsigned)((n_ws + 255) / 256), 256, 0, s>>>(ws, n_ws, 0u);
+  dim3 rgrid((unsigned)(n_pages < 64 ? n_pages : 64), (unsigned)n_planes);
+  if (bf16)
+    int4_channel_absmax_kernel<true><<<rgrid, kThreads, 0, s>>>(
+        cache_planes, cache_page_stride, block_ids, pool_pages, n_pages, g, ws, err_flag);
+  else
+    int4_channel_absmax_kernel<false><<<rgrid, kThreads, 0, s>>>(
+        cache_planes, cache_page_stride, block_ids, pool_pages, n_pages, g, ws, err_flag);
+  if (bf16)
+    int4_channel_quant_gather_kernel<true><<<grid, kThreads, 0, s>>>(
+        cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, g, ws, err_flag);
+  else
+    int4_channel_quant_gather_kernel<false><<<grid, kThreads, 0, s>>>(
+        cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, g, ws, err_flag);
+  dim3 fgrid((unsigned)((head_dim + 255) / 256), (unsigned)n_planes);
+  int4_channel_finalize_kernel<<<fgrid, 256, 0, s>>>(param_planes, ws, n_planes, g.pps, head_dim);
+  return check_launch(who);
+}

@@ -1,0 +1,141 @@
+// amf_kernel_util.h - device-side building blocks shared by the codec and
+// decode kernels: 16-element cache-row loads/stores, fp8/bf16/fp16
+// conversions and division helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "amf_device.h"
+
+namespace amf {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---- cache element <-> fp32 -------------------------------------------------
+
+// Low / high 16-bit halves of a dword as fp32, for a bf16 or fp16 cache.
+template <bool BF16>
+__device__ __forceinline__ float half_lo(uint32_t w) {
+  if constexpr (BF16) {
+    return u2f(w << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+  }
+}
+template <bool BF16>
+__device__ __forceinline__ float half_hi(uint32_t w) {
+  if constexpr (BF16) {
+    return u2f(w & 0xFFFF0000u);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+}
+
+// Keeps an fp32 value materialised: without it the compiler may fold a
+// preceding multiply into the fp16 conversion (v_fma_mix*_f16 with a +0
+// addend), which rounds once instead of fp32-then-fp16 and turns -0 into +0.
+__device__ __forceinline__ void keep_f32(float& x) { asm("" : "+v"(x)); }
+
+// Two fp32 -> one dword of cache elements, round to nearest even
+// (v_cvt_pk_bf16_f32 for bf16, v_cvt_f16_f32 for fp16).
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (!BF16) {
+    keep_f32(a);
+    keep_f32(b);
+  }
+  if constexpr (BF16) {
+    uint32_t lo = __builtin_bit_cast(uint16_t, (__bf16)a);
+    uint32_t hi = __builtin_bit_cast(uint16_t, (__bf16)b);
+    return lo | (hi << 16);
+  } else {
+    uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)a);
+    uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)b);
+    return lo | (hi << 16);
+  }
+}
+
+// 8 cache elements (one 16-byte vector) -> fp32.
+template <bool BF16>
+__device__ __forceinline__ void unpack8(const u32x4& v, float* x) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = half_lo<BF16>(v[i]);
+    x[2 * i + 1] = half_hi<BF16>(v[i]);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ u32x4 pack8(const float* x) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack2<BF16>(x[2 * i], x[2 * i + 1]);
+  return r;
+}
+
+// ---- fp8 e4m3fn -------------------------------------------------------------
+
+// Four e4m3 codes (one dword) -> fp32, exact.  Uses gfx950's OCP-format
+// v_cvt_pk_f32_fp8 when AMF_FP8_HW_DECODE is set, otherwise the fp16
+// widening trick of e4m3x2_to_f16x2_scaled with an explicit 2^8 rescale.
+__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* out) {
+#if AMF_FP8_HW_DECODE
+  f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  out[0] = a[0];
+  out[1] = a[1];
+  out[2] = b[0];
+  out[3] = b[1];
+#else
+  uint32_t lo = e4m3x2_to_f16x2_scaled(w & 0xFFFFu);
+  uint32_t hi = e4m3x2_to_f16x2_scaled(w >> 16);
+  out[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(lo & 0xFFFFu)) * 256.0f;
+  out[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(lo >> 16)) * 256.0f;
+  out[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(hi & 0xFFFFu)) * 256.0f;
+  out[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(hi >> 16)) * 256.0f;
+#endif
+}
+
+// Four fp32 (already clamped to [-448, 448]) -> four e4m3fn codes in a dword.
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(const float* x) {
+#if AMF_FP8_HW_ENCODE
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], w, true);
+  return (uint32_t)w;
+#else
+  return e4m3_from_f32(x[0]) | (e4m3_from_f32(x[1]) << 8) | (e4m3_from_f32(x[2]) << 16) |
+         (e4m3_from_f32(x[3]) << 24);
+#endif
+}
+
+// ---- division ---------------------------------------------------------------
+
+// x / b rounded to nearest even (IEEE).  rb must be the correctly rounded
+// reciprocal RN(1/b).  With AMF_MARKSTEIN_DIV the quotient comes from
+// Markstein's sequence q = RN(x*rb), r = x - b*q (exact via fma),
+// q' = RN(q + r*rb), which returns RN(x/b) for normal operands when rb is
+// RN(1/b) (Markstein 1990; Muller et al., Handbook of Floating-Point
+// Arithmetic, Thm. 4.10); otherwise the compiler's correctly rounded divide.
+__device__ __forceinline__ float div_rn(float x, float b, float rb) {
+#if AMF_MARKSTEIN_DIV
+  float q = x * rb;
+  float r = __builtin_fmaf(-q, b, x);
+  return __builtin_fmaf(r, rb, q);
+#else
+  (void)rb;
+  return x / b;
+#endif
+}
+
+// ---- small reductions -------------------------------------------------------
+
+__device__ __forceinline__ float wave_max_xor(float v, int width) {
+  for (int o = width / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, width));
+  return v;
+}
+
+}  // namespace amf

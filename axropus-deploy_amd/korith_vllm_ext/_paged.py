@@ -1,0 +1,370 @@
+"""_paged.py - host-side plumbing between torch tensors and libamf_hip.so.
+
+Describes a vLLM paged KV cache as "planes" (one K or V array of one layer),
+lays out a compressed blob (codes + params of every plane of one layer, one
+contiguous span), builds the device address tables the kernels take, and
+launches the gather/scatter and codec entry points on torch's current stream.
+
+Blob layout for `n` pages of geometry (block_size bs, heads H, head_dim D)
+and P planes (P = 2 for a vLLM layer: K then V):
+
+    [plane 0 codes][plane 1 codes]...[pad to 16][params]
+
+params are either one region shared by every plane (fp8_e4m3's FP8ScaleSidecar,
+int4_sym's per-channel scales) or one 16-byte-aligned region per plane.  The
+byte formats of codes and params are the AMF_FMT_* layouts of
+include/amf_hip.h.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+import amf_hip
+
+# ---------------------------------------------------------------- formats --
+
+FMT_FP8_E4M3 = "fp8_e4m3"
+FMT_FP8_E4M3_PH = "fp8_e4m3_ph"
+FMT_INT4_SYM = "int4_sym"
+FMT_INT4_BLOCK = "int4_sym_block"
+FMT_INT4_ASYM_G32 = "int4_asym_g32"
+
+_FMT_IDS = {
+    FMT_FP8_E4M3: amf_hip.FMT_FP8_E4M3,
+    FMT_FP8_E4M3_PH: amf_hip.FMT_FP8_E4M3_PH,
+    FMT_INT4_BLOCK: amf_hip.FMT_INT4_SYM_BLOCK,
+    FMT_INT4_SYM: amf_hip.FMT_INT4_SYM,
+    FMT_INT4_ASYM_G32: amf_hip.FMT_INT4_ASYM_G32,
+}
+
+PAGED_FORMATS = tuple(_FMT_IDS)
+
+# Tokens per page a dense (unpaged) [.., T, H, D] tensor is cut into.  The
+# reference's INT4PerBlockCodec blocks 128 tokens (amf_codec.py:353); the
+# other formats are indifferent to paging and use vLLM's 16.
+DENSE_PAGE_TOKENS = {
+    FMT_FP8_E4M3: 16,
+    FMT_FP8_E4M3_PH: 16,
+    FMT_INT4_BLOCK: 128,
+    FMT_INT4_SYM: 16,
+    FMT_INT4_ASYM_G32: 16,
+}
+
+
+def _align16(n: int) -> int:
+    return (n + 15) // 16 * 16
+
+
+@dataclass(frozen=True)
+class BlobLayout:
+    """Byte layout of one compressed blob (n_pages pages of n_planes planes)."""
+
+    fmt: str
+    n_planes: int
+    n_pages: int
+    block_size: int
+    num_heads: int
+    head_dim: int
+
+    @property
+    def fmt_id(self) -> int:
+        return _FMT_IDS[self.fmt]
+
+    @property
+    def family(self) -> str:
+        return "fp8" if self.fmt.startswith("fp8") else "int4"
+
+    @property
+    def page_elems(self) -> int:
+        return self.block_size * self.num_heads * self.head_dim
+
+    @property
+    def code_bytes_per_page(self) -> int:
+        return self.page_elems if self.family == "fp8" else self.page_elems // 2
+
+    @property
+    def plane_code_bytes(self) -> int:
+        return self.n_pages * self.code_bytes_per_page
+
+    @property
+    def data_bytes(self) -> int:
+        return self.n_planes * self.plane_code_bytes
+
+    @property
+    def shared_params(self) -> bool:
+        return self.fmt in (FMT_FP8_E4M3, FMT_INT4_SYM)
+
+    @property
+    def plane_param_bytes(self) -> int:
+        """Param bytes of one plane (0 for the shared-param formats)."""
+        n, H, D = self.n_pages, self.num_heads, self.head_dim
+        if self.fmt == FMT_FP8_E4M3_PH:
+            return n * H * 4
+        if self.fmt == FMT_INT4_BLOCK:
+            return n * 2
+        if self.fmt == FMT_INT4_ASYM_G32:
+            return n * H * self.block_size * (D // 32) * 4
+        return 0
+
+    @property
+    def shared_param_bytes(self) -> int:
+        if self.fmt == FMT_FP8_E4M3:
+            return 16  # [k_scale, v_scale, q_scale, prob_scale] fp32
+        if self.fmt == FMT_INT4_SYM:
+            return self.head_dim * 2
+        return 0
+
+    @property
+    def scale_offset(self) -> int:
+        return _align16(self.data_bytes)
+
+    @property
+    def scale_bytes(self) -> int:
+        if self.shared_params:
+            return self.shared_param_bytes
+        return (self.n_planes - 1) * _align16(self.plane_param_bytes) + self.plane_param_bytes
+
+    @property
+    def total_bytes(self) -> int:
+        return self.scale_offset + self.scale_bytes
+
+    def code_offset(self, plane: int) -> int:
+        return plane * self.plane_code_bytes
+
+    def param_offset(self, plane: int) -> int:
+        if self.shared_params:
+            return self.scale_offset
+        return self.scale_offset + plane * _align16(self.plane_param_bytes)
+
+    def validate(self) -> None:
+        if self.fmt not in _FMT_IDS:
+            raise KeyError(f"format {self.fmt!r} has no paged kernel")
+        if self.head_dim % 32:
+            raise ValueError(f"head_dim {self.head_dim} must be a multiple of 32")
+        if self.fmt == FMT_INT4_ASYM_G32:
+            if self.block_size != 16:
+                raise ValueError("int4_asym_g32 pages hold 16 tokens")
+            if self.n_planes % 2:
+                raise ValueError("int4_asym_g32 needs (K, V) plane pairs")
+
+
+# ------------------------------------------------------------- cache view --
+
+
+@dataclass
+class CacheView:
+    """A list of per-layer KV tensors seen as planes (K0, V0, K1, V1, ...).
+
+    Accepted per-layer shapes (compressed_vram_pool.py:483-486):
+      [2, num_blocks, block_size, H, D]  stacked K/V (vLLM >= 0.6)
+      [num_blocks, block_size, H, D]     one array used for both K and V
+    Each page must be contiguous ([block_size][H][D] row-major).
+    """
+
+    planes: List[int]
+    page_stride: int  # bytes
+    pool_pages: int
+    block_size: int
+    num_heads: int
+    head_dim: int
+    dtype: torch.dtype
+    device: torch.device
+    keep: list = field(default_factory=list, repr=False)
+
+    @property
+    def n_layers(self) -> int:
+        return len(self.planes) // 2
+
+    @property
+    def page_bytes(self) -> int:
+        return self.block_size * self.num_heads * self.head_dim * _elem_size(self.dtype)
+
+
+def _elem_size(dtype: torch.dtype) -> int:
+    return torch.empty((), dtype=dtype).element_size()
+
+
+def _kv_of(layer: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    if layer.dim() == 5 and layer.shape[0] == 2:
+        return layer[0], layer[1]
+    if layer.dim() == 4:
+        return layer, layer
+    raise ValueError(
+        f"KV cache layer of shape {tuple(layer.shape)}: expected [2, num_blocks, block_size, H, D]"
+        " or [num_blocks, block_size, H, D]"
+    )
+
+
+def cache_view(gpu_cache: Sequence[torch.Tensor]) -> CacheView:
+    if len(gpu_cache) == 0:
+        raise ValueError("empty KV cache")
+    planes: List[int] = []
+    geom = None
+    for layer in gpu_cache:
+        for t in _kv_of(layer):
+            nb, bs, H, D = t.shape
+            es = t.element_size()
+            if t.stride(3) != 1 or t.stride(2) != D or t.stride(1) != H * D:
+                raise ValueError("KV cache pages must be contiguous [block_size][H][D]")
+            g = (nb, bs, H, D, t.stride(0) * es, t.dtype, t.device)
+            if geom is None:
+                geom = g
+            elif g != geom:
+                raise ValueError(f"KV cache layers differ in geometry: {g} vs {geom}")
+            planes.append(t.data_ptr())
+    nb, bs, H, D, stride, dtype, device = geom
+    return CacheView(planes, stride, nb, bs, H, D, dtype, device, keep=list(gpu_cache))
+
+
+def dense_view(x: torch.Tensor, page_tokens: int) -> Tuple[CacheView, int, torch.Tensor]:
+    """View a contiguous [..., T, H, D] tensor as planes of pages.
+
+    Leading dims become planes.  T is zero-padded to a multiple of page_tokens
+    (a copy; zero rows change no absmax and are dropped on the way back).
+    Returns (view, n_pages, padded tensor kept alive by the view).
+    """
+    if x.dim() < 3:
+        raise ValueError(f"expected [..., tokens, heads, head_dim], got {tuple(x.shape)}")
+    T, H, D = x.shape[-3:]
+    P = int(math.prod(x.shape[:-3])) if x.dim() > 3 else 1
+    xp = x.reshape(P, T, H, D)
+    n_pages = max(1, -(-T // page_tokens))
+    Tp = n_pages * page_tokens
+    if Tp != T or not xp.is_contiguous():
+        pad = torch.zeros((P, Tp, H, D), dtype=x.dtype, device=x.device)
+        pad[:, :T].copy_(xp)
+        xp = pad
+    es = xp.element_size()
+    page_stride = page_tokens * H * D * es
+    planes = [xp.data_ptr() + p * Tp * H * D * es for p in range(P)]
+    v = CacheView(planes, page_stride, n_pages, page_tokens, H, D, xp.dtype, xp.device, keep=[xp])
+    return v, n_pages, xp
+
+
+# ---------------------------------------------------------------- launches --
+
+
+def _device_ids(ids, device) -> Optional[torch.Tensor]:
+    if ids is None:
+        return None
+    if isinstance(ids, torch.Tensor):
+        t = ids.to(device=device, dtype=torch.int32)
+    else:
+        t = torch.tensor(list(ids), dtype=torch.int32, device=device)
+    return t.contiguous()
+
+
+def check_block_ids(ids: Sequence[int], pool_pages: int, *, unique: bool) -> None:
+    """Host-side validation of a block table (ValueError, like the reference's
+    shape checks) so that the kernels' in-kernel skip never has to trigger."""
+    import numpy as np
+
+    a = np.asarray(list(ids), dtype=np.int64)
+    if a.size == 0:
+        return
+    if a.min() < 0 or a.max() >= pool_pages:
+        raise ValueError(f"block id out of range [0, {pool_pages}): min {a.min()} max {a.max()}")
+    if unique and np.unique(a).size != a.size:
+        raise ValueError("duplicate block ids in a scatter target")
+
+
+def _ptr(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else int(t.data_ptr())
+
+
+def gather_pages(view: CacheView, block_ids, out_planes: Sequence[int], out_page_stride: int,
+                 n_pages: int, err_flag: Optional[torch.Tensor] = None) -> None:
+    dev = view.device
+    ids = _device_ids(block_ids, dev)
+    src = amf_hip.address_table(view.planes, dev)
+    dst = amf_hip.address_table(out_planes, dev)
+    amf_hip.call(
+        "amf_kv_gather_pages", _ptr(src), view.page_stride, _ptr(ids), view.pool_pages, _ptr(dst),
+        out_page_stride, len(view.planes), n_pages, view.page_bytes, _ptr(err_flag),
+        amf_hip.stream_handle(dev),
+    )
+
+
+def scatter_pages(in_planes: Sequence[int], in_page_stride: int, view: CacheView, block_ids,
+                  n_pages: int, err_flag: Optional[torch.Tensor] = None) -> None:
+    dev = view.device
+    ids = _device_ids(block_ids, dev)
+    src = amf_hip.address_table(in_planes, dev)
+    dst = amf_hip.address_table(view.planes, dev)
+    amf_hip.call(
+        "amf_kv_scatter_pages", _ptr(src), in_page_stride, _ptr(dst), view.page_stride, _ptr(ids),
+        view.pool_pages, len(view.planes), n_pages, view.page_bytes, _ptr(err_flag),
+        amf_hip.stream_handle(dev),
+    )
+
+
+@dataclass
+class PlaneTables:
+    """Device address tables of one codec launch (kept alive until enqueued)."""
+
+    codes: torch.Tensor
+    params: torch.Tensor
+
+
+def blob_tables(layout: BlobLayout, blob_bases: Sequence[int], planes_per_blob: int,
+                device) -> PlaneTables:
+    """Code/param plane tables for blobs at `blob_bases` (one blob per group of
+    planes_per_blob planes)."""
+    codes, params = [], []
+    for base in blob_bases:
+        for p in range(planes_per_blob):
+            codes.append(base + layout.code_offset(p))
+            params.append(base + layout.param_offset(p))
+    return PlaneTables(amf_hip.address_table(codes, device), amf_hip.address_table(params, device))
+
+
+def quant_gather(layout: BlobLayout, view: CacheView, block_ids, blob_bases: Sequence[int],
+                 planes_per_blob: int, workspace: Optional[torch.Tensor] = None,
+                 err_flag: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
+    """Gather + quantize every plane of `view` into the blobs at blob_bases.
+
+    Returns the workspace (it holds each scale group's absmax bits for the
+    shared-scale formats after the launch)."""
+    layout.validate()
+    dev = view.device
+    n_planes = len(view.planes)
+    if n_planes != planes_per_blob * len(blob_bases):
+        raise ValueError("plane count does not match the blobs")
+    tables = blob_tables(layout, blob_bases, planes_per_blob, dev)
+    ids = _device_ids(block_ids, dev)
+    ws_bytes = amf_hip.quant_workspace_bytes(layout.fmt_id, n_planes, planes_per_blob, view.head_dim)
+    if ws_bytes and (workspace is None or workspace.numel() * 4 < ws_bytes):
+        workspace = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)
+    fn = "amf_fp8_quant_gather" if layout.family == "fp8" else "amf_int4_quant_gather"
+    amf_hip.call(
+        fn, layout.fmt_id, _ptr(amf_hip.address_table(view.planes, dev)), view.page_stride,
+        amf_hip.dtype_tag(view.dtype), _ptr(ids), view.pool_pages, _ptr(tables.codes),
+        _ptr(tables.params), n_planes, planes_per_blob, layout.n_pages, view.block_size,
+        view.num_heads, view.head_dim, _ptr(workspace),
+        0 if workspace is None else workspace.numel() * 4, _ptr(err_flag),
+        amf_hip.stream_handle(dev),
+    )
+    return workspace
+
+
+def dequant_scatter(layout: BlobLayout, blob_bases: Sequence[int], planes_per_blob: int,
+                    view: CacheView, block_ids, err_flag: Optional[torch.Tensor] = None) -> None:
+    layout.validate()
+    dev = view.device
+    n_planes = len(view.planes)
+    if n_planes != planes_per_blob * len(blob_bases):
+        raise ValueError("plane count does not match the blobs")
+    tables = blob_tables(layout, blob_bases, planes_per_blob, dev)
+    ids = _device_ids(block_ids, dev)
+    fn = "amf_fp8_dequant_scatter" if layout.family == "fp8" else "amf_int4_dequant_scatter"
+    amf_hip.call(
+        fn, layout.fmt_id, _ptr(tables.codes), _ptr(tables.params),
+        _ptr(amf_hip.address_table(view.planes, dev)), view.page_stride,
+        amf_hip.dtype_tag(view.dtype), _ptr(ids), view.pool_pages, n_planes, layout.n_pages,
+        view.block_size, view.num_heads, view.head_dim, _ptr(err_flag), amf_hip.stream_handle(dev),
+    )

@@ -1,0 +1,251 @@
+/*
+ * amf_hip.h - C ABI of libamf_hip.so, the gfx950 (MI355X) implementation of
+ * the Axropus AMF KV-materialization hot path.
+ *
+ * Scope: paged gather/scatter between a vLLM-style paged KV cache and the AMF
+ * VRAM tier, the FP8 (e4m3fn) and INT4 codecs of the compressed VRAM pool
+ * (quantize-on-save, dequantize+scatter-on-restore), and paged GQA decode
+ * attention that reads INT4 KV with fused dequantization.
+ *
+ * Conventions shared by every entry point
+ * ---------------------------------------
+ *  - All pointers except `stream` are DEVICE addresses; sizes are int64/int32.
+ *  - A "plane" is one K or V array of one layer.  Plane arrays (`*_planes`)
+ *    are device arrays of n_planes uint64 base addresses, normally ordered
+ *    (K of layer 0, V of layer 0, K of layer 1, ...).  Page p of a cache plane
+ *    starts at planes[i] + p * page_stride (bytes) and holds
+ *    block_size * num_heads * head_dim elements in [token][head][dim] order
+ *    (vLLM's [num_blocks, block_size, num_kv_heads, head_size] page).
+ *  - `block_ids` (int32, device, n_pages entries) maps a position in the
+ *    gathered sequence to a physical page of the cache.  NULL means the
+ *    identity map (contiguous, unpaged source or destination).
+ *  - Every page whose block id lies outside [0, pool_pages) is skipped (never
+ *    read or written); the kernel then ORs AMF_ERRFLAG_BLOCK_RANGE into
+ *    *err_flag when err_flag is not NULL.  Duplicate ids in a scatter target
+ *    leave those pages holding one of the writers' values (unspecified which);
+ *    nothing faults.
+ *  - `stream` is a hipStream_t (NULL = default stream).  Every call is
+ *    stream-ordered, allocates no device memory, keeps no state between
+ *    calls and may be issued from any host thread.
+ *  - Return value: AMF_OK (0) or a negative AMF_ERR_* code; the message for
+ *    the calling thread's last failure is returned by amf_last_error().
+ *    Nothing throws across this boundary.
+ *
+ * Interfaces replaced (reference file:line):
+ *  - korith_vllm_ext/compressed_vram_pool.py:434-560  put_from_vllm gather+compress
+ *  - korith_vllm_ext/compressed_vram_pool.py:562-608  restore_to_vllm decompress+scatter
+ *  - korith_vllm_ext/amf_kv_manager.py:298-321, 488-523  raw page gather / scatter
+ *  - korith_vllm_ext/codecs/amf_codec.py:174-222      FP8E4M3Codec compress/decompress_to
+ *  - korith_vllm_ext/codecs/amf_codec.py:292-447      INT4PerChannelCodec / INT4PerBlockCodec
+ *  - korith_vllm_ext/codecs/amf_codec.py:502-539      _pack_int4 / _unpack_int4
+ *  - korith_vllm_ext/int4_decode_attention.py:6-9 -> kernels/dispatch.py:117-143
+ *    (int4_decode_attention; the CUDA kernel it was meant to reach is
+ *    korith_vllm_ext/kernels/int4_decode_attention.cu:39-213, bound at
+ *    korith_vllm_ext/kernels/bindings.cpp:64-76)
+ */
+#ifndef AMF_HIP_H
+#define AMF_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AMF_ABI_VERSION 1
+
+/* ---- status codes ------------------------------------------------------ */
+#define AMF_OK                  0
+#define AMF_ERR_INVALID_ARG    (-1)  /* null pointer, negative size, bad enum */
+#define AMF_ERR_UNSUPPORTED    (-2)  /* shape/format this build does not implement */
+#define AMF_ERR_LAUNCH         (-3)  /* the HIP runtime rejected a launch */
+#define AMF_ERR_WORKSPACE      (-4)  /* workspace missing or too small */
+
+/* bits ORed into *err_flag by kernels */
+#define AMF_ERRFLAG_BLOCK_RANGE 1    /* a block id was outside [0, pool_pages) */
+#define AMF_ERRFLAG_CONTEXT     2    /* a context length exceeded its block table */
+
+/* ---- element types: same numbering as the AMFK header dtype field
+ *      (core/amf_direct_kv.h AmfKvDtype; amf_kv_manager.py:60-64) --------- */
+#define AMF_DTYPE_F16   0
+#define AMF_DTYPE_F32   1
+#define AMF_DTYPE_BF16  2
+
+/* ---- codec formats ------------------------------------------------------
+ * Layouts are per plane; n_pages pages of one plane are contiguous.
+ *
+ * AMF_FMT_FP8_E4M3 (reference "fp8_e4m3", amf_codec.py:174-222)
+ *   codes  : [n_pages][block_size][num_heads][head_dim] e4m3fn bytes
+ *   params : the scale group's fp32 sidecar [k_scale, v_scale, q_scale,
+ *            prob_scale] (FP8ScaleSidecar, amf_codec.py:62-94).  A scale
+ *            group is `planes_per_scale` consecutive planes (2 = the K and V
+ *            of one layer) whose param_planes entries all hold the address of
+ *            that group's sidecar; save writes the group's scale to slots 0
+ *            and 1 and 1.0 to slots 2 and 3; restore reads slot (plane & 1).
+ *   scale  = max(absmax over the group, floor) / 448, floor = 1e-8 rounded
+ *            to the cache dtype; code = e4m3fn_rne(clamp(x / scale, -448, 448))
+ *            (division by 1e-12 when the floored absmax is 0);
+ *   x'     = to_cache_dtype(fp32(code) * scale).
+ * AMF_FMT_FP8_E4M3_PH (per-(page, head) scale; no reference counterpart)
+ *   codes  : as AMF_FMT_FP8_E4M3
+ *   params : [n_pages][num_heads] fp32 scales
+ *   scale  = max(absmax over the page's block_size x head_dim values of that
+ *            head, 1e-8f) / 448; codes and x' as above.
+ * AMF_FMT_INT4_SYM_BLOCK (reference "int4_sym_block" on a page tensor,
+ *   amf_codec.py:345-447): one fp16 scale per page over all heads
+ *   codes  : [n_pages][block_size][num_heads][head_dim/2] bytes, byte i of a
+ *            row = (u[2i+1] << 4) | u[2i], u = q + 8 (amf_codec.py:502-521)
+ *   params : [n_pages] fp16; scale32 = max(absmax_page, 1e-8f) / 7,
+ *            q = clamp(rint(x / scale32), -8, 7), stored fp16(scale32);
+ *   x'     = to_cache_dtype(fp32(q) * fp32(fp16 scale)).
+ * AMF_FMT_INT4_SYM (reference "int4_sym", amf_codec.py:292-343): one fp16
+ *   scale per head_dim channel over a scale group of `planes_per_scale`
+ *   planes (2 = K and V of a layer) whose param_planes entries all hold the
+ *   address of the group's [head_dim] fp16 scales.
+ *   codes as AMF_FMT_INT4_SYM_BLOCK; scale32_d = max(absmax_d, 1e-8f) / 7.
+ * AMF_FMT_INT4_ASYM_G32 (no reference counterpart): asymmetric, one fp16
+ *   (scale, zero) pair per (token, head, 32-dim group); G = head_dim / 32.
+ *   Pages are head-major; within a (page, head) block of block_size = 16:
+ *   K codes : [16 tokens][head_dim/2] bytes, byte i = dims 2i (low nibble)
+ *             and 2i+1 (high nibble)
+ *   V codes : dim-major tiles: for dim d and token t the nibble lives in
+ *             byte 64*(d/8) + 32*(t/8) + 4*(d%8) + (t%8)/2, low nibble for
+ *             even t.  (One 32-byte run = 8 tokens x 8 dims.)
+ *   K params: [16 tokens][G] uint32, low half fp16 scale, high half fp16 zero
+ *   V params: [G][16 tokens] uint32, same packing
+ *   mn, mx  = min, max of the group (fp32);
+ *   scale32 = max(mx - mn, 1e-8f) / 15;  q = clamp(rint((x - mn) / scale32), 0, 15);
+ *   stored  (fp16(scale32), fp16(mn));   x' = to_cache_dtype(q * s16 + z16)
+ *   with an unfused fp32 multiply then add.
+ * All divisions are IEEE correctly rounded; rint rounds half to even.
+ */
+#define AMF_FMT_FP8_E4M3        1
+#define AMF_FMT_FP8_E4M3_PH     2
+#define AMF_FMT_INT4_SYM_BLOCK  3
+#define AMF_FMT_INT4_SYM        4
+#define AMF_FMT_INT4_ASYM_G32   5
+
+/* ABI version of the loaded library (AMF_ABI_VERSION when it was built). */
+int amf_abi_version(void);
+
+/* Message describing the calling thread's last failed call ("" if none). */
+const char* amf_last_error(void);
+
+/* Bytes of fp32 workspace that amf_*_quant_gather needs for `format`
+ * (cross-page reductions of AMF_FMT_FP8_E4M3 and AMF_FMT_INT4_SYM: one slot,
+ * or head_dim slots, per scale group); 0 for formats reduced within a page. */
+int64_t amf_quant_workspace_bytes(int32_t format, int32_t n_planes, int32_t planes_per_scale,
+                                  int32_t head_dim);
+
+/* Raw paged gather (snapshot): out_planes[i] page j <- cache_planes[i] page
+ * block_ids[j], for i < n_planes, j < n_pages; page_bytes bytes each (a
+ * multiple of 16, all strides and bases 16-byte aligned).
+ * Replaces k_all[block_ids] / v_all[block_ids] in
+ * compressed_vram_pool.py:491-504 and amf_kv_manager.py:311-318. */
+int amf_kv_gather_pages(const uint64_t* cache_planes, int64_t cache_page_stride,
+                        const int32_t* block_ids, int64_t pool_pages,
+                        const uint64_t* out_planes, int64_t out_page_stride,
+                        int32_t n_planes, int64_t n_pages, int64_t page_bytes,
+                        int32_t* err_flag, void* stream);
+
+/* Raw paged scatter (restore): cache_planes[i] page block_ids[j] <-
+ * in_planes[i] page j.  Replaces k_all[chunk_ids] = src in
+ * compressed_vram_pool.py:599-606 and amf_kv_manager.py:505-523. */
+int amf_kv_scatter_pages(const uint64_t* in_planes, int64_t in_page_stride,
+                         const uint64_t* cache_planes, int64_t cache_page_stride,
+                         const int32_t* block_ids, int64_t pool_pages,
+                         int32_t n_planes, int64_t n_pages, int64_t page_bytes,
+                         int32_t* err_flag, void* stream);
+
+/* Save path: gather n_pages pages of each cache plane through block_ids and
+ * quantize them into code_planes / param_planes in `format` (an AMF_FMT_FP8_*
+ * value).  planes_per_scale (>= 1, dividing n_planes) groups planes for the
+ * per-tensor format and is ignored otherwise.  cache_dtype is AMF_DTYPE_BF16 or AMF_DTYPE_F16.  workspace: device
+ * fp32 buffer of amf_quant_workspace_bytes() bytes (may be NULL when that is
+ * 0); its contents on entry do not matter.
+ * Replaces compressed_vram_pool.py:481-508 with FP8E4M3Codec.compress
+ * (amf_codec.py:186-209). */
+int amf_fp8_quant_gather(int32_t format,
+                         const uint64_t* cache_planes, int64_t cache_page_stride,
+                         int32_t cache_dtype, const int32_t* block_ids, int64_t pool_pages,
+                         const uint64_t* code_planes, const uint64_t* param_planes,
+                         int32_t n_planes, int32_t planes_per_scale, int64_t n_pages,
+                         int32_t block_size, int32_t num_heads, int32_t head_dim,
+                         float* workspace, int64_t workspace_bytes,
+                         int32_t* err_flag, void* stream);
+
+/* Restore path: dequantize n_pages pages of each plane and scatter them into
+ * the cache pages block_ids[j].  Replaces compressed_vram_pool.py:579-606
+ * with FP8E4M3Codec.decompress_to (amf_codec.py:211-222). */
+int amf_fp8_dequant_scatter(int32_t format,
+                            const uint64_t* code_planes, const uint64_t* param_planes,
+                            const uint64_t* cache_planes, int64_t cache_page_stride,
+                            int32_t cache_dtype, const int32_t* block_ids, int64_t pool_pages,
+                            int32_t n_planes, int64_t n_pages,
+                            int32_t block_size, int32_t num_heads, int32_t head_dim,
+                            int32_t* err_flag, void* stream);
+
+/* INT4 save path (format = AMF_FMT_INT4_*).  Replaces
+ * compressed_vram_pool.py:481-508 with INT4PerBlockCodec.compress
+ * (amf_codec.py:358-408) / INT4PerChannelCodec.compress (:305-330). */
+int amf_int4_quant_gather(int32_t format,
+                          const uint64_t* cache_planes, int64_t cache_page_stride,
+                          int32_t cache_dtype, const int32_t* block_ids, int64_t pool_pages,
+                          const uint64_t* code_planes, const uint64_t* param_planes,
+                          int32_t n_planes, int32_t planes_per_scale, int64_t n_pages,
+                          int32_t block_size, int32_t num_heads, int32_t head_dim,
+                          float* workspace, int64_t workspace_bytes,
+                          int32_t* err_flag, void* stream);
+
+/* INT4 restore path.  Replaces compressed_vram_pool.py:579-606 with
+ * INT4PerBlockCodec.decompress_to (amf_codec.py:410-447) /
+ * INT4PerChannelCodec.decompress_to (:332-343). */
+int amf_int4_dequant_scatter(int32_t format,
+                             const uint64_t* code_planes, const uint64_t* param_planes,
+                             const uint64_t* cache_planes, int64_t cache_page_stride,
+                             int32_t cache_dtype, const int32_t* block_ids, int64_t pool_pages,
+                             int32_t n_planes, int64_t n_pages,
+                             int32_t block_size, int32_t num_heads, int32_t head_dim,
+                             int32_t* err_flag, void* stream);
+
+/* ---- paged GQA decode attention over AMF_FMT_INT4_ASYM_G32 pages --------
+ * q, out     : [num_seqs][num_q_heads][head_dim]; q_dtype is AMF_DTYPE_BF16
+ *              or AMF_DTYPE_F16, out_dtype one of those or AMF_DTYPE_F32
+ * k_codes, k_params, v_codes, v_params : one layer's INT4_ASYM_G32 planes of
+ *              pool_pages pages each (page strides implied by the geometry)
+ * block_tables: [num_seqs][block_table_stride] int32; context_lens: [num_seqs]
+ * Query head h attends KV head h / (num_q_heads / num_kv_heads).
+ * max_context_len bounds every context_lens[i] (it sizes the grid: no
+ * device-to-host sync); a sequence with context 0 gets zeros.
+ * softmax_scale <= 0 selects 1/sqrt(head_dim).
+ * workspace: split-K partials, amf_int4_decode_workspace_bytes() bytes.
+ * algo: AMF_DECODE_AUTO, AMF_DECODE_VALU or AMF_DECODE_MFMA.
+ * Supported: head_dim 128, block_size 16, num_q_heads / num_kv_heads in
+ * {1, 2, 4, 8}; anything else returns AMF_ERR_UNSUPPORTED.
+ * Replaces int4_decode_attention (int4_decode_attention.py:6-9 ->
+ * dispatch.py:117-143), adding paging and GQA. */
+#define AMF_DECODE_AUTO  0
+#define AMF_DECODE_VALU  1
+#define AMF_DECODE_MFMA  2
+
+int64_t amf_int4_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                        int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t max_context_len);
+
+int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* out, int32_t out_dtype,
+                               const void* k_codes, const void* k_params,
+                               const void* v_codes, const void* v_params,
+                               int64_t pool_pages,
+                               const int32_t* block_tables, int32_t block_table_stride,
+                               const int32_t* context_lens,
+                               int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t block_size,
+                               int32_t max_context_len, float softmax_scale,
+                               void* workspace, int64_t workspace_bytes,
+                               int32_t algo, int32_t* err_flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AMF_HIP_H */
