@@ -368,3 +368,56 @@ def dequant_scatter(layout: BlobLayout, blob_bases: Sequence[int], planes_per_bl
         amf_hip.dtype_tag(view.dtype), _ptr(ids), view.pool_pages, n_planes, layout.n_pages,
         view.block_size, view.num_heads, view.head_dim, _ptr(err_flag), amf_hip.stream_handle(dev),
     )
+
+
+class PreparedCodecLaunch:
+    """A dequant-scatter or quant-gather with its device tables built once.
+
+    Repeated launches (a pool entry restored into the same cache, a timed
+    loop) then cost one ctypes call each.  The object keeps every tensor the
+    kernel reads alive."""
+
+    def __init__(self, direction: str, layout: BlobLayout, blob_bases: Sequence[int],
+                 planes_per_blob: int, view: CacheView, block_ids,
+                 err_flag: Optional[torch.Tensor] = None) -> None:
+        if direction not in ("save", "restore"):
+            raise ValueError(direction)
+        layout.validate()
+        dev = view.device
+        n_planes = len(view.planes)
+        if n_planes != planes_per_blob * len(blob_bases):
+            raise ValueError("plane count does not match the blobs")
+        self.direction = direction
+        self.layout = layout
+        self.view = view
+        self.tables = blob_tables(layout, blob_bases, planes_per_blob, dev)
+        self.cache_tab = amf_hip.address_table(view.planes, dev)
+        self.ids = _device_ids(block_ids, dev)
+        self.err_flag = err_flag
+        self.planes_per_blob = planes_per_blob
+        self.workspace = None
+        ws_bytes = amf_hip.quant_workspace_bytes(layout.fmt_id, n_planes, planes_per_blob,
+                                                 view.head_dim)
+        if direction == "save" and ws_bytes:
+            self.workspace = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)
+        fam = layout.family
+        self.fn = f"amf_{fam}_quant_gather" if direction == "save" else f"amf_{fam}_dequant_scatter"
+        self._cfn = getattr(amf_hip.load(), self.fn)
+
+    def launch(self, stream: Optional[int] = None) -> None:
+        v, lay = self.view, self.layout
+        s = amf_hip.stream_handle(v.device) if stream is None else stream
+        if self.direction == "save":
+            ws = self.workspace
+            rc = self._cfn(lay.fmt_id, _ptr(self.cache_tab), v.page_stride,
+                           amf_hip.dtype_tag(v.dtype), _ptr(self.ids), v.pool_pages,
+                           _ptr(self.tables.codes), _ptr(self.tables.params), len(v.planes),
+                           self.planes_per_blob, lay.n_pages, v.block_size, v.num_heads,
+                           v.head_dim, _ptr(ws), 0 if ws is None else ws.numel() * 4,
+                           _ptr(self.err_flag), s)
+        else:
+            rc = self._cfn(lay.fmt_id, _ptr(self.tables.codes), _ptr(self.tables.params),
+                           _ptr(self.cache_tab), v.page_stride, amf_hip.dtype_tag(v.dtype),
+                           _ptr(self.ids), v.pool_pages, len(v.planes), lay.n_pages,
+                           v.block_size, v.num_heads, v.head_dim, _ptr(self.err_flag), s)
+        amf_hip.check(self.fn, rc)

@@ -1,0 +1,102 @@
+"""Parity at the benchmark's full sizes, checked on samples.
+
+The inputs are exactly the ones bench.py times (its case builders are
+reused): the Llama-3-8B FP8 restore (32 layers, 512 pages into 8192) and INT4
+restore (2048 pages into 16384), and the batch-32 INT4 paged decode with
+contexts U[1024, 32768].  Restored layers are compared bit-for-bit with the
+oracle on sampled layers plus size-independent properties over all layers
+(untouched pool pages keep their sentinel; the restored pages of every layer
+round-trip through the oracle decompress of that layer's blob is sampled).
+Decode is compared with float64 attention on sampled sequences.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import attention as oatt
+from oracle import codecs as oc
+
+from helpers import attn_errors
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+def _oracle_restore(case: "bench.RestoreCase", l: int) -> torch.Tensor:
+    lay = case.layout
+    blob = case.blobs[l].cpu()
+    if case.fmt == "fp8_e4m3_ph":
+        codes = blob[:lay.data_bytes].view(2, case.pages, 16, case.heads, case.head_dim)
+        sc = torch.stack([blob[lay.param_offset(p):lay.param_offset(p) + lay.plane_param_bytes]
+                          .view(torch.float32).view(case.pages, case.heads) for p in range(2)])
+        return oc.fp8_ph_decompress(codes, sc, torch.bfloat16)
+    cpl = lay.plane_code_bytes
+    c = torch.stack([blob[lay.code_offset(p):lay.code_offset(p) + cpl].view(case.pages, -1)
+                     for p in range(2)])
+    pr = torch.stack([blob[lay.param_offset(p):lay.param_offset(p) + lay.plane_param_bytes]
+                      .view(torch.int32).view(case.pages, -1).to(torch.int64) & 0xFFFFFFFF
+                      for p in range(2)])
+    return oc.int4_asym_decompress(c, pr, 16, case.heads, case.head_dim, torch.bfloat16)
+
+
+@pytest.mark.parametrize("fmt", ["fp8_e4m3_ph", "int4_asym_g32"])
+def test_restore_fullsize(fmt):
+    if fmt == "fp8_e4m3_ph":
+        case = bench.RestoreCase(fmt, 32, 8, 128, 8192, 512, seed=2)
+    else:
+        case = bench.RestoreCase(fmt, 32, 8, 128, 16384, 2048, seed=3)
+    sentinel = torch.tensor(-3.5, dtype=torch.bfloat16)
+    for c in case.cache:
+        c.fill_(sentinel.item())
+    case.launch.launch()
+    torch.cuda.synchronize()
+    ids = case.ids.long().to(DEV)
+    mask = torch.ones(case.pool, dtype=torch.bool, device=DEV)
+    mask[ids] = False
+    for l in range(case.layers):
+        # every layer: untouched pages still hold the sentinel
+        assert bool((case.cache[l][:, mask] == sentinel.item()).all()), f"layer {l}"
+    for l in (0, 13, case.layers - 1):
+        want = _oracle_restore(case, l)
+        got = case.cache[l][:, ids].cpu()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"layer {l}"
+    case.free()
+
+
+def test_decode_fullsize_sampled():
+    import amf_hip
+
+    dc = bench.DecodeCase()
+    for algo in (amf_hip.DECODE_MFMA, amf_hip.DECODE_VALU):
+        dc.launch(algo)
+        torch.cuda.synchronize()
+        out = dc.out.float().cpu().numpy()
+        lay = dc.layout
+        cpp = lay.code_bytes_per_page
+        ppp = lay.plane_param_bytes // dc.pool
+        for b in (0, 7, dc.batch - 1):
+            n = (int(dc.ctx[b]) + 15) // 16
+            pages = dc.bt_cpu[b, :n].long().tolist()
+            codes, params = [], []
+            for p in range(2):
+                cbase, pbase = lay.code_offset(p), lay.param_offset(p)
+                codes.append(torch.stack([dc.blob[cbase + pg * cpp: cbase + (pg + 1) * cpp]
+                                          for pg in pages]).cpu())
+                params.append(torch.stack([dc.blob[pbase + pg * ppp: pbase + (pg + 1) * ppp]
+                                           for pg in pages]).cpu().view(torch.int32)
+                              .to(torch.int64) & 0xFFFFFFFF)
+            u, s16, z16 = oc.int4_asym_unlayout(torch.stack(codes), torch.stack(params), 16,
+                                                dc.kv_heads, dc.D)
+            kv32 = oc.int4_asym_dequant_f32(u, s16, z16).numpy()
+            ref = oatt.paged_decode_f64(dc.q[b:b + 1].float().cpu().numpy(), kv32[0], kv32[1],
+                                        np.arange(n)[None], dc.ctx[b:b + 1].numpy())
+            # bf16 output: its own rounding (half an ulp, <= |ref| 2^-8) on top of 2e-2
+            half_ulp = np.abs(ref) * 2.0 ** -8
+            d = np.abs(out[b:b + 1] - ref)
+            assert float((d - (2e-2 + half_ulp)).max()) <= 0.0, (algo, b, float(d.max()))
+            _, mean_rel = attn_errors(out[b:b + 1], ref)
+            assert mean_rel <= 1e-2, (algo, b, mean_rel)
