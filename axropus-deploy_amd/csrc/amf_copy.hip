@@ -9,10 +9,13 @@
 // UNROLL loads in flight before the matching stores, so a 4 KiB page is one
 // trip of 256 lanes and a 32 KiB page four trips of two batches.
 #include "amf_internal.h"
+#include "amf_kernel_util.h"
 
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+using amf::u32x4;
+using amf::ld_stream;
+using amf::st_stream;
 
 constexpr int kThreads = 256;
 constexpr int kUnroll = 4;
@@ -37,12 +40,12 @@ __global__ __launch_bounds__(kThreads) void page_copy_kernel(
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       int64_t k = base + (int64_t)u * kThreads;
-      if (k < n16) v[u] = __builtin_nontemporal_load(s + k);
+      if (k < n16) v[u] = ld_stream(s + k);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       int64_t k = base + (int64_t)u * kThreads;
-      if (k < n16) __builtin_nontemporal_store(v[u], d + k);
+      if (k < n16) st_stream(v[u], d + k);
     }
   }
 }

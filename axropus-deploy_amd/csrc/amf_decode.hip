@@ -184,6 +184,67 @@ __device__ __forceinline__ int64_t page_of(const DecodeArgs& a, const int32_t* b
   return *ok ? (int64_t)v : 0;
 }
 
+// Loads of one 32-token chunk (two pages) for the MFMA lane layout.
+struct ChunkLoads {
+  u32x4 kcode[2], kpar[2];  // K codes / params of page u: lane (t = lo, j = hi)
+  u32x4 vc0, vc1;           // V codes: lane (dim block lo, tokens 8 hi .. 8 hi + 7)
+  u32x4 vp0, vp1;           // V params of group lo % 4 for those 8 tokens
+};
+
+__device__ __forceinline__ ChunkLoads issue_chunk(const DecodeArgs& a, int64_t pg0, int64_t pg1,
+                                                  int h, int lo, int hi) {
+  ChunkLoads c;
+  const int H = a.num_kv_heads;
+  const int64_t hb0 = pg0 * H + h, hb1 = pg1 * H + h;
+  c.kcode[0] = *reinterpret_cast<const u32x4*>(a.kc + hb0 * kHBCodes + lo * 64 + hi * 16);
+  c.kcode[1] = *reinterpret_cast<const u32x4*>(a.kc + hb1 * kHBCodes + lo * 64 + hi * 16);
+  c.kpar[0] = *reinterpret_cast<const u32x4*>(a.kp + hb0 * kHBParams + lo * 4);
+  c.kpar[1] = *reinterpret_cast<const u32x4*>(a.kp + hb1 * kHBParams + lo * 4);
+  const int64_t vhb = (hi >> 1) ? hb1 : hb0;
+  const u32x4* vcp =
+      reinterpret_cast<const u32x4*>(a.vc + vhb * kHBCodes + 64 * lo + 32 * (hi & 1));
+  c.vc0 = vcp[0];
+  c.vc1 = vcp[1];
+  const u32x4* vpp =
+      reinterpret_cast<const u32x4*>(a.vp + vhb * kHBParams + (lo & 3) * 16 + 8 * (hi & 1));
+  c.vp0 = vpp[0];
+  c.vp1 = vpp[1];
+  return c;
+}
+
+// Block-table entries of a split (at most 64 pages: split_tokens <= 1024),
+// one per lane; chunk code reads them back with readlane (wave-uniform).
+struct SplitPages {
+  int v;      // this lane's physical page id (or -1)
+  int first;  // logical page index of lane 0
+};
+
+__device__ __forceinline__ SplitPages load_split_pages(const DecodeArgs& a, const int32_t* bt,
+                                                      int tok_begin, int tok_end) {
+  SplitPages sp;
+  sp.first = tok_begin / kBS;
+  const int n = (tok_end - tok_begin + kBS - 1) / kBS;
+  const int lane = threadIdx.x;
+  int v = -1;
+  if (lane < n) {
+    v = bt[sp.first + lane];
+    if ((v < 0 || (int64_t)v >= a.pool_pages)) {
+      if (a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+      v = -2;  // invalid id: masked, never dereferenced
+    }
+  }
+  sp.v = v;
+  return sp;
+}
+
+// Physical page of logical page pi of the split, page 0 when it is outside
+// the context or invalid (ok = false).
+__device__ __forceinline__ int64_t split_page(const SplitPages& sp, int pi, bool* ok) {
+  const int v = __builtin_amdgcn_readlane(sp.v, pi - sp.first);
+  *ok = v >= 0;
+  return v >= 0 ? (int64_t)v : 0;
+}
+
 // ============================================================== MFMA path ==
 
 template <int R, bool QBF16>
@@ -256,27 +317,27 @@ __global__ __launch_bounds__(64) void int4_decode_mfma_kernel(DecodeArgs a) {
   }
   __shared__ __attribute__((aligned(16))) float p_lds[NT][2][4][16];
 
-  for (int c0 = tok_begin; c0 < tok_end; c0 += 32) {
-    const int pi0 = c0 / kBS;
-    bool pok[2];
-    int64_t pg[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) pg[u] = page_of(a, bt, pi0 + u, (pi0 + u) * kBS < tok_end, &pok[u]);
+  // Software pipeline: the next chunk's pages are in flight while the current
+  // chunk computes.  The last iteration re-loads its own chunk (clamped).
+  const SplitPages spg = load_split_pages(a, bt, tok_begin, tok_end);
+  const int last_c0 = tok_begin + ((tok_end - tok_begin - 1) / 32) * 32;
+  bool pok_n[2];
+  int64_t pg_n[2];
+  pg_n[0] = split_page(spg, tok_begin / kBS, &pok_n[0]);
+  pg_n[1] = split_page(spg, tok_begin / kBS + 1, &pok_n[1]);
+  ChunkLoads nxt = issue_chunk(a, pg_n[0], pg_n[1], h, lo, hi);
 
-    // ---- loads: K (codes + params) of both pages, V codes + params ----
-    u32x4 kcode[2], kpar[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t hb = pg[u] * H + h;
-      kcode[u] = *reinterpret_cast<const u32x4*>(a.kc + hb * kHBCodes + lo * 64 + hi * 16);
-      kpar[u] = *reinterpret_cast<const u32x4*>(a.kp + hb * kHBParams + lo * 4);
-    }
+  for (int c0 = tok_begin; c0 < tok_end; c0 += 32) {
+    const ChunkLoads cur = nxt;
+    bool pok[2] = {pok_n[0], pok_n[1]};
+    const int cn = c0 + 32 <= last_c0 ? c0 + 32 : c0;
+    pg_n[0] = split_page(spg, cn / kBS, &pok_n[0]);
+    pg_n[1] = split_page(spg, cn / kBS + 1, &pok_n[1]);
+    nxt = issue_chunk(a, pg_n[0], pg_n[1], h, lo, hi);
+    const u32x4* kcode = cur.kcode;
+    const u32x4* kpar = cur.kpar;
     const int vu = hi >> 1, vhalf = hi & 1;
-    const int64_t vhb = pg[vu] * H + h;
-    const u32x4* vcp = reinterpret_cast<const u32x4*>(a.vc + vhb * kHBCodes + 64 * lo + 32 * vhalf);
-    const u32x4 vc0 = vcp[0], vc1 = vcp[1];
-    const u32x4* vpp = reinterpret_cast<const u32x4*>(a.vp + vhb * kHBParams + (lo & 3) * 16 + 8 * vhalf);
-    const u32x4 vp0 = vpp[0], vp1 = vpp[1];
+    const u32x4 vc0 = cur.vc0, vc1 = cur.vc1, vp0 = cur.vp0, vp1 = cur.vp1;
 
     // ---- QK^T and online softmax ----
     float x[NT][2];
@@ -557,7 +618,8 @@ __global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
 // ================================================================ merge ====
 
 // One wave per (query head, sequence): O = sum_i 2^(m_i - M) acc_i / L,
-// written as OUT_DTYPE (an AMF_DTYPE_* tag).
+// written as OUT_DTYPE (an AMF_DTYPE_* tag).  Split statistics are read one
+// split per lane (up to 64 per pass), the accumulators two dims per lane.
 template <int OUT_DTYPE>
 __global__ __launch_bounds__(64) void int4_decode_merge_kernel(DecodeArgs a) {
   const int qhd = blockIdx.x, s = blockIdx.y;
@@ -566,15 +628,30 @@ __global__ __launch_bounds__(64) void int4_decode_merge_kernel(DecodeArgs a) {
   const int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
   const float* base = a.ws + ((int64_t)s * a.num_q_heads + qhd) * a.max_splits * kPartStride;
   float M = kNegBig;
-  for (int i = 0; i < n_sp; ++i) M = fmaxf(M, base[(int64_t)i * kPartStride + kD]);
-  float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int i = 0; i < n_sp; ++i) {
-    const float* p = base + (int64_t)i * kPartStride;
-    const float w = exp2_fast(p[kD] - M);
-    L += w * p[kD + 1];
-    o0 += w * p[2 * lane];
-    o1 += w * p[2 * lane + 1];
+  for (int i0 = 0; i0 < n_sp; i0 += 64) {
+    const int i = i0 + lane;
+    if (i < n_sp) M = fmaxf(M, base[(int64_t)i * kPartStride + kD]);
   }
+  M = wave_max_xor(M, 64);
+  float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (int i0 = 0; i0 < n_sp; i0 += 64) {
+    const int i = i0 + lane;
+    float w = 0.0f;
+    if (i < n_sp) {
+      const float* p = base + (int64_t)i * kPartStride;
+      w = exp2_fast(p[kD] - M);
+      L += w * p[kD + 1];
+    }
+    const int cnt = min(64, n_sp - i0);
+    for (int k = 0; k < cnt; ++k) {
+      const float wk = __shfl(w, k);
+      const float* p = base + (int64_t)(i0 + k) * kPartStride;
+      const float2 v = *reinterpret_cast<const float2*>(p + 2 * lane);
+      o0 += wk * v.x;
+      o1 += wk * v.y;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   const int64_t row = ((int64_t)s * a.num_q_heads + qhd) * kD;
   if constexpr (OUT_DTYPE == AMF_DTYPE_F32) {
@@ -591,13 +668,14 @@ __global__ __launch_bounds__(64) void int4_decode_merge_kernel(DecodeArgs a) {
 // Split size: a multiple of 32 tokens chosen so that about kTargetWaves waves
 // of work exist when every sequence is max_context_len long.
 constexpr int64_t kTargetWaves = 8192;
+constexpr int kMaxSplitTokens = 1024;  // 64 pages: one block-table entry per lane
 
 int choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context_len) {
   const int64_t work = (int64_t)num_seqs * num_kv_heads * (max_context_len > 0 ? max_context_len : 1);
   int64_t split = (work + kTargetWaves - 1) / kTargetWaves;
   split = (split + 31) / 32 * 32;
   if (split < 256) split = 256;
-  if (split > 4096) split = 4096;
+  if (split > kMaxSplitTokens) split = kMaxSplitTokens;
   return (int)split;
 }
 

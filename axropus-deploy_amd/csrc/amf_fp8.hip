@@ -46,6 +46,10 @@ __device__ __forceinline__ float tensor_floor() {
 
 // ---------------------------------------------------------------- restore --
 
+// One lane = one 8-element chunk (8 code bytes in, one 16-byte vector of
+// cache elements out), so each wave-wide store covers 1 KiB contiguously and
+// every cache line is written whole.  The chunk's head is fixed per lane when
+// 2048 elements (one workgroup pass) span whole rows of heads.
 template <bool BF16, bool PER_TENSOR>
 __global__ __launch_bounds__(kThreads) void fp8_dequant_scatter_kernel(
     const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
@@ -58,42 +62,41 @@ __global__ __launch_bounds__(kThreads) void fp8_dequant_scatter_kernel(
     if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
     return;
   }
-  const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
+  const int page_elems = g.n_rows * g.head_dim;
+  const int n8 = page_elems >> 3;
   const uint8_t* __restrict__ codes =
-      reinterpret_cast<const uint8_t*>(code_planes[plane]) + j * page_elems;
+      reinterpret_cast<const uint8_t*>(code_planes[plane]) + j * (int64_t)page_elems;
   const float* __restrict__ params = reinterpret_cast<const float*>(param_planes[plane]);
   uint8_t* __restrict__ out = reinterpret_cast<uint8_t*>(cache_planes[plane]) + dp * cache_stride;
-
-  const int col = lane_col(g), rpi = rows_per_iter(g);
-  const float tscale = PER_TENSOR ? params[plane & 1] : 0.0f;
   const float* __restrict__ page_scales = params + j * g.num_heads;
-  const float hscale = PER_TENSOR ? tscale : page_scales[lane_row0(g) % g.num_heads];
+  const int tid = threadIdx.x;
+  float s_fixed = 0.0f;
+  if (PER_TENSOR)
+    s_fixed = params[plane & 1];
+  else if (g.head_const)
+    s_fixed = page_scales[((tid * 8) / g.head_dim) % g.num_heads];
 
-  constexpr int U = 4;
-  for (int r = lane_row0(g); r < g.n_rows; r += U * rpi) {
-    u32x4 c[U];
+  constexpr int U = AMF_RESTORE_UNROLL;
+  for (int base = tid; base < n8; base += U * kThreads) {
+    u32x2 c[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row = r + u * rpi;
-      if (row < g.n_rows) {
-        const int64_t e = (int64_t)row * g.head_dim + col * 16;
-        c[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + e));
-      }
+      const int k = base + u * kThreads;
+      if (k < n8) c[u] = ld_stream(reinterpret_cast<const u32x2*>(codes) + k);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row = r + u * rpi;
-      if (row < g.n_rows) {
-        float s = PER_TENSOR ? tscale : (g.head_const ? hscale : page_scales[row % g.num_heads]);
-        float x[16];
+      const int k = base + u * kThreads;
+      if (k < n8) {
+        const float s = (PER_TENSOR || g.head_const)
+                            ? s_fixed
+                            : page_scales[((k * 8) / g.head_dim) % g.num_heads];
+        float x[8];
+        e4m3x4_to_f32(c[u][0], x);
+        e4m3x4_to_f32(c[u][1], x + 4);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) e4m3x4_to_f32(c[u][q], x + 4 * q);
-#pragma unroll
-        for (int q = 0; q < 16; ++q) x[q] = x[q] * s;
-        const int64_t e = (int64_t)row * g.head_dim + col * 16;
-        u32x4* dst = reinterpret_cast<u32x4*>(out + 2 * e);
-        __builtin_nontemporal_store(pack8<BF16>(x), dst);
-        __builtin_nontemporal_store(pack8<BF16>(x + 8), dst + 1);
+        for (int q = 0; q < 8; ++q) x[q] = x[q] * s;
+        st_stream(pack8<BF16>(x), reinterpret_cast<u32x4*>(out) + k);
       }
     }
   }
@@ -259,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void fp8_quant_gather_kernel(
       u32x4 c;
 #pragma unroll
       for (int q = 0; q < 4; ++q) c[q] = f32x4_to_e4m3(x + 4 * q);
-      __builtin_nontemporal_store(
+      st_stream(
           c, reinterpret_cast<u32x4*>(codes + (int64_t)row * g.head_dim + col * 16));
     }
   }
@@ -276,7 +279,9 @@ int make_geom(const char* who, int32_t block_size, int32_t num_heads, int32_t he
   g->head_dim = head_dim;
   g->num_heads = num_heads;
   g->cpr_log2 = __builtin_ctz(cpr);
-  g->head_const = ((kThreads / cpr) % num_heads) == 0;
+  // Restore passes advance 8 * kThreads elements; save passes kThreads / cpr rows.
+  g->head_const = ((kThreads * 8) % (head_dim * num_heads)) == 0 &&
+                  ((kThreads / cpr) % num_heads) == 0;
   g->pps = pps > 0 ? pps : 1;
   return ok();
 }

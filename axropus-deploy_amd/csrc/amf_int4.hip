@@ -52,11 +52,13 @@ template <bool BF16>
 __device__ __forceinline__ void store32(uint8_t* p, const float* x) {
   u32x4* v = reinterpret_cast<u32x4*>(p);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) __builtin_nontemporal_store(pack8<BF16>(x + 8 * q), v + q);
+  for (int q = 0; q < 4; ++q) st_stream(pack8<BF16>(x + 8 * q), v + q);
 }
 
 // CHANNEL = false: INT4_SYM_BLOCK (params: [n_pages] fp16);
-// CHANNEL = true : INT4_SYM       (params: [head_dim] fp16 per layer).
+// CHANNEL = true : INT4_SYM       (params: [head_dim] fp16 per scale group).
+// One lane = one 8-element chunk (4 code bytes in, one 16-byte vector out):
+// wave-wide stores cover 1 KiB contiguously.
 template <bool BF16, bool CHANNEL>
 __global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
     const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
@@ -69,42 +71,38 @@ __global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
     if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
     return;
   }
-  const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
-  const uint8_t* __restrict__ codes =
-      reinterpret_cast<const uint8_t*>(code_planes[plane]) + j * (page_elems / 2);
+  const int page_elems = g.n_rows * g.head_dim;
+  const int n8 = page_elems >> 3;
+  const uint32_t* __restrict__ codes =
+      reinterpret_cast<const uint32_t*>(code_planes[plane]) + j * (int64_t)n8;
   const _Float16* __restrict__ params = reinterpret_cast<const _Float16*>(param_planes[plane]);
   uint8_t* __restrict__ out = reinterpret_cast<uint8_t*>(cache_planes[plane]) + dp * cache_stride;
-  const int col = sym_col(g), rpi = sym_rpi(g);
-
-  float s_page = CHANNEL ? 0.0f : (float)params[j];
-  float s_ch[32];
+  const int tid = threadIdx.x;
+  const float s_page = CHANNEL ? 0.0f : (float)params[j];
+  // Channel scales of this lane's 8 dims; fixed while 8 * kThreads is a
+  // multiple of head_dim (checked on the host).
+  float s_ch[8];
   if (CHANNEL) {
+    const int d0 = (tid * 8) % g.head_dim;
 #pragma unroll
-    for (int q = 0; q < 32; ++q) s_ch[q] = (float)params[col * 32 + q];
+    for (int q = 0; q < 8; ++q) s_ch[q] = (float)params[d0 + q];
   }
-  constexpr int U = 4;
-  for (int r = sym_row0(g); r < g.n_rows; r += U * rpi) {
-    u32x4 c[U];
+  constexpr int U = AMF_RESTORE_UNROLL;
+  for (int base = tid; base < n8; base += U * kThreads) {
+    uint32_t c[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row = r + u * rpi;
-      if (row < g.n_rows)
-        c[u] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(codes + ((int64_t)row * g.head_dim + col * 32) / 2));
+      const int k = base + u * kThreads;
+      if (k < n8) c[u] = ld_stream(codes + k);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row = r + u * rpi;
-      if (row < g.n_rows) {
-        float x[32];
+      const int k = base + u * kThreads;
+      if (k < n8) {
+        float x[8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int n = 0; n < 8; ++n) {
-            const float qv = nib(c[u][q], n) - 8.0f;
-            x[8 * q + n] = qv * (CHANNEL ? s_ch[8 * q + n] : s_page);
-          }
-        store32<BF16>(out + 2 * ((int64_t)row * g.head_dim + col * 32), x);
+        for (int n = 0; n < 8; ++n) x[n] = (nib(c[u], n) - 8.0f) * (CHANNEL ? s_ch[n] : s_page);
+        st_stream(pack8<BF16>(x), reinterpret_cast<u32x4*>(out) + k);
       }
     }
   }
@@ -179,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void int4_symblock_quant_gather_kernel(
         }
         c[q] = w;
       }
-      __builtin_nontemporal_store(
+      st_stream(
           c, reinterpret_cast<u32x4*>(codes + ((int64_t)row * g.head_dim + col * 32) / 2));
     }
   }
@@ -266,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void int4_channel_quant_gather_kernel(
       }
       c[q] = w;
     }
-    __builtin_nontemporal_store(
+    st_stream(
         c, reinterpret_cast<u32x4*>(codes + ((int64_t)r * g.head_dim + col * 32) / 2));
   }
 }
@@ -360,21 +358,23 @@ __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
   uint8_t* __restrict__ out = reinterpret_cast<uint8_t*>(cache_planes[plane]) + dp * cache_stride;
 
   if (!is_v) {
-    const int n_items = H * 16 * G;
+    // Items (token, head, 8-dim block) in cache order: lane k writes the k-th
+    // 16-byte vector of the page, reads 4 code bytes and its group's param word.
+    const int kpr = D / 8;  // 8-dim blocks per row
+    const int n_items = 16 * H * kpr;
     for (int it = threadIdx.x; it < n_items; it += kThreads) {
-      const int gi = it % G;
-      const int ht = it / G;  // head * 16 + token
-      const int h = ht >> 4, t = ht & 15;
-      const u32x4 c = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(codes + (int64_t)ht * (D / 2) + 16 * gi));
-      const uint32_t pw = params[ht * G + gi];
+      const int kk = it % kpr;
+      const int th = it / kpr;  // token * H + head
+      const int t = th / H, h = th % H;
+      const int ht = h * 16 + t;
+      const uint32_t c = ld_stream(
+          reinterpret_cast<const uint32_t*>(codes + (int64_t)ht * (D / 2)) + kk);
+      const uint32_t pw = params[ht * G + (kk >> 2)];
       const float s = param_scale(pw), z = param_zero(pw);
-      float x[32];
+      float x[8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int n = 0; n < 8; ++n) x[8 * q + n] = nib(c[q], n) * s + z;
-      store32<BF16>(out + 2 * ((int64_t)(t * H + h) * D + 32 * gi), x);
+      for (int n = 0; n < 8; ++n) x[n] = nib(c, n) * s + z;
+      st_stream(pack8<BF16>(x), reinterpret_cast<u32x4*>(out) + it);
     }
   } else {
     const int nb = D / 8;
@@ -385,8 +385,8 @@ __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
       const int h = (it >> 1) / nb;
       const u32x4* cp =
           reinterpret_cast<const u32x4*>(codes + (int64_t)h * g.hb_code_bytes + 64 * b + 32 * th);
-      const u32x4 c0 = __builtin_nontemporal_load(cp);
-      const u32x4 c1 = __builtin_nontemporal_load(cp + 1);
+      const u32x4 c0 = ld_stream(cp);
+      const u32x4 c1 = ld_stream(cp + 1);
       const uint32_t w[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
       const u32x4* pp = reinterpret_cast<const u32x4*>(params + h * g.hb_param_words +
                                                        (b >> 2) * 16 + 8 * th);
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
 #pragma unroll
         for (int k = 0; k < 8; ++k) x[k] = nib(w[k], i) * s + z;
         const int t = 8 * th + i;
-        __builtin_nontemporal_store(
+        st_stream(
             pack8<BF16>(x),
             reinterpret_cast<u32x4*>(out + 2 * ((int64_t)(t * H + h) * D + 8 * b)));
       }
@@ -432,7 +432,7 @@ __device__ __forceinline__ void asym_quant_k(const uint8_t* __restrict__ src,
       c[q] = w;
     }
     const int ht = h * 16 + t;
-    __builtin_nontemporal_store(c,
+    st_stream(c,
                                 reinterpret_cast<u32x4*>(codes + (int64_t)ht * (D / 2) + 16 * gi));
     params[ht * G + gi] = asym_param_word(p);
   }
@@ -495,8 +495,8 @@ __device__ __forceinline__ void asym_quant_v(const uint8_t* __restrict__ src,
       for (int k = 0; k < 8; ++k) w[k] |= asym_code(x[k], p) << (4 * i);
     }
     u32x4* cp = reinterpret_cast<u32x4*>(codes + (int64_t)h * g.hb_code_bytes + 64 * b + 32 * th);
-    __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]}, cp);
-    __builtin_nontemporal_store(u32x4{w[4], w[5], w[6], w[7]}, cp + 1);
+    st_stream(u32x4{w[0], w[1], w[2], w[3]}, cp);
+    st_stream(u32x4{w[4], w[5], w[6], w[7]}, cp + 1);
   }
 }
 
@@ -601,8 +601,10 @@ extern "C" int amf_int4_dequant_scatter(int32_t format, const uint64_t* code_pla
   }
   SymGeom g;
   if ((rc = make_sym_geom(who, block_size, num_heads, head_dim, 1, &g))) return rc;
-  if (n_pages == 0) return ok();
   const bool ch = format == AMF_FMT_INT4_SYM;
+  if (ch && (8 * kThreads) % head_dim != 0)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: head_dim %d must divide %d", who, head_dim, 8 * kThreads);
+  if (n_pages == 0) return ok();
 #define AMF_LAUNCH(B, C)                                                                        \
   int4_sym_dequant_scatter_kernel<B, C><<<grid, kThreads, 0, s>>>(                              \
       code_planes, param_planes, cache_planes, cache_page_stride, block_ids, pool_pages, g, \

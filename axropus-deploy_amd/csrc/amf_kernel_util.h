@@ -15,6 +15,36 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// ---- streaming loads / stores -------------------------------------------------
+// Data read or written once per launch (codes, restored pages) goes through
+// these; AMF_USE_NT selects the non-temporal cache policy.
+#ifndef AMF_USE_NT
+#define AMF_USE_NT 1
+#endif
+
+// Loads a restore lane keeps in flight before its stores.
+#ifndef AMF_RESTORE_UNROLL
+#define AMF_RESTORE_UNROLL 4
+#endif
+
+template <typename T>
+__device__ __forceinline__ T ld_stream(const T* p) {
+#if AMF_USE_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
+template <typename T>
+__device__ __forceinline__ void st_stream(const T& v, T* p) {
+#if AMF_USE_NT
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
+
 // ---- cache element <-> fp32 -------------------------------------------------
 
 // Low / high 16-bit halves of a dword as fp32, for a bf16 or fp16 cache.

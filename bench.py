@@ -287,7 +287,7 @@ def main() -> int:
             fn = lambda: _paged.gather_pages(view, None, [dst.data_ptr(), dst.data_ptr()],
                                              view.page_bytes, 32768)
             ms = time_launches(fn, args.steps, args.warmup)
-            log(f"copy: {ms:.4f} ms/launch for 2 x 2 GiB moved")
+            log(f"copy: {ms:.4f} ms/launch, 2 GiB read + 2 GiB written per launch")
             return 0
         if args.profile in ("fp8_restore", "int4_restore"):
             fmt = "fp8_e4m3_ph" if args.profile == "fp8_restore" else "int4_asym_g32"
