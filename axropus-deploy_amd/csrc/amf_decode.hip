@@ -247,8 +247,13 @@ __device__ __forceinline__ int64_t split_page(const SplitPages& sp, int pi, bool
 
 // ============================================================== MFMA path ==
 
+#ifndef AMF_DECODE_WAVES_PER_EU
+#define AMF_DECODE_WAVES_PER_EU 2
+#endif
+
 template <int R, bool QBF16>
-__global__ __launch_bounds__(64) void int4_decode_mfma_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(AMF_DECODE_WAVES_PER_EU)))
+void int4_decode_mfma_kernel(DecodeArgs a) {
   constexpr int NT = (R + 3) / 4;  // 16-row tiles of (head, group) pairs
   const int sp = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
   const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
@@ -665,14 +670,21 @@ __global__ __launch_bounds__(64) void int4_decode_merge_kernel(DecodeArgs a) {
   }
 }
 
-// Split size: a multiple of 32 tokens chosen so that about kTargetWaves waves
-// of work exist when every sequence is max_context_len long.
-constexpr int64_t kTargetWaves = 8192;
+// Split size: a multiple of 32 tokens in [256, 1024] chosen so that about
+// kTargetWaves waves of work exist when every sequence is max_context_len
+// long, with at most kMaxSplitsPerSeq splits per sequence.
+#ifndef AMF_DECODE_TARGET_WAVES
+#define AMF_DECODE_TARGET_WAVES 32768
+#endif
+constexpr int64_t kTargetWaves = AMF_DECODE_TARGET_WAVES;
 constexpr int kMaxSplitTokens = 1024;  // 64 pages: one block-table entry per lane
+constexpr int kMaxSplitsPerSeq = 128;  // bounds the merge's reads of partials
 
 int choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context_len) {
   const int64_t work = (int64_t)num_seqs * num_kv_heads * (max_context_len > 0 ? max_context_len : 1);
   int64_t split = (work + kTargetWaves - 1) / kTargetWaves;
+  const int64_t per_seq = ((int64_t)max_context_len + kMaxSplitsPerSeq - 1) / kMaxSplitsPerSeq;
+  if (split < per_seq) split = per_seq;
   split = (split + 31) / 32 * 32;
   if (split < 256) split = 256;
   if (split > kMaxSplitTokens) split = kMaxSplitTokens;

@@ -221,6 +221,24 @@ def cache_view(gpu_cache: Sequence[torch.Tensor]) -> CacheView:
     return CacheView(planes, stride, nb, bs, H, D, dtype, device, keep=list(gpu_cache))
 
 
+def planes_view(planes: Sequence[torch.Tensor]) -> CacheView:
+    """One plane per [num_blocks, block_size, H, D] tensor (contiguous pages)."""
+    addrs = []
+    geom = None
+    for t in planes:
+        nb, bs, H, D = t.shape
+        if t.stride(3) != 1 or t.stride(2) != D or t.stride(1) != H * D:
+            raise ValueError("plane pages must be contiguous [block_size][H][D]")
+        g = (nb, bs, H, D, t.stride(0) * t.element_size(), t.dtype, t.device)
+        if geom is None:
+            geom = g
+        elif g != geom:
+            raise ValueError("planes differ in geometry")
+        addrs.append(t.data_ptr())
+    nb, bs, H, D, stride, dtype, device = geom
+    return CacheView(addrs, stride, nb, bs, H, D, dtype, device, keep=list(planes))
+
+
 def dense_view(x: torch.Tensor, page_tokens: int) -> Tuple[CacheView, int, torch.Tensor]:
     """View a contiguous [..., T, H, D] tensor as planes of pages.
 
