@@ -94,6 +94,11 @@ SIGNATURES = {
          _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_ptr, _c_i64, _c_i32, _c_ptr,
          _c_ptr],
     ),
+    "amf_dense_attn": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_ptr, _c_i32, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i32,
+         _c_i64, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_ptr],
+    ),
 }
 
 

@@ -45,7 +45,7 @@ constexpr int kD = 128;          // head_dim
 constexpr int kBS = 16;          // tokens per page
 constexpr int kHBCodes = 1024;   // code bytes of one (page, head) block
 constexpr int kHBParams = 64;    // param words of one (page, head) block
-constexpr int kPartStride = kD + 2;  // split partial: D accumulators, m, l
+constexpr int kPartStride = kD + 4;  // split partial: D accumulators, m, l, 2 pad (16-byte rows)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1.0e30f;
 
@@ -262,7 +262,6 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
   if (tok_begin >= ctx) return;
   const int tok_end = min(ctx, tok_begin + a.split_tokens);
   const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
-  const int H = a.num_kv_heads;
   const uint16_t* qh = a.q + ((int64_t)s * a.num_q_heads + (int64_t)h * R) * kD;
 
   // ---- Q operands (constant for the wave) ----
@@ -622,41 +621,70 @@ __global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
 
 // ================================================================ merge ====
 
-// One wave per (query head, sequence): O = sum_i 2^(m_i - M) acc_i / L,
-// written as OUT_DTYPE (an AMF_DTYPE_* tag).  Split statistics are read one
-// split per lane (up to 64 per pass), the accumulators two dims per lane.
+// One workgroup of four waves per (query head, sequence):
+// O = sum_i 2^(m_i - M) acc_i / L, written as OUT_DTYPE (an AMF_DTYPE_* tag).
+// Split statistics are read one split per thread and the weights shared
+// through LDS; wave w sums the accumulators of splits w, w+4, ... (two dims per
+// lane, several splits in flight), and the four wave sums meet in LDS.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeWaves = kMergeThreads / 64;
+
 template <int OUT_DTYPE>
-__global__ __launch_bounds__(64) void int4_decode_merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(DecodeArgs a) {
+  __shared__ float wgt[kMergeThreads];
+  __shared__ float red[kMergeWaves][kD];
+  __shared__ float sred[kMergeWaves];
   const int qhd = blockIdx.x, s = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int ctx = clamp_context(a, s);
   const int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
   const float* base = a.ws + ((int64_t)s * a.num_q_heads + qhd) * a.max_splits * kPartStride;
   float M = kNegBig;
-  for (int i0 = 0; i0 < n_sp; i0 += 64) {
-    const int i = i0 + lane;
-    if (i < n_sp) M = fmaxf(M, base[(int64_t)i * kPartStride + kD]);
-  }
+  for (int i = tid; i < n_sp; i += kMergeThreads) M = fmaxf(M, base[(int64_t)i * kPartStride + kD]);
   M = wave_max_xor(M, 64);
+  if (lane == 0) sred[w] = M;
+  __syncthreads();
+  M = sred[0];
+#pragma unroll
+  for (int i = 1; i < kMergeWaves; ++i) M = fmaxf(M, sred[i]);
   float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int i0 = 0; i0 < n_sp; i0 += 64) {
-    const int i = i0 + lane;
-    float w = 0.0f;
+  for (int i0 = 0; i0 < n_sp; i0 += kMergeThreads) {
+    __syncthreads();  // sred / wgt of the previous pass are consumed
+    const int i = i0 + tid;
+    float wi = 0.0f;
     if (i < n_sp) {
       const float* p = base + (int64_t)i * kPartStride;
-      w = exp2_fast(p[kD] - M);
-      L += w * p[kD + 1];
+      wi = exp2_fast(p[kD] - M);
+      L += wi * p[kD + 1];
     }
-    const int cnt = min(64, n_sp - i0);
-    for (int k = 0; k < cnt; ++k) {
-      const float wk = __shfl(w, k);
-      const float* p = base + (int64_t)(i0 + k) * kPartStride;
-      const float2 v = *reinterpret_cast<const float2*>(p + 2 * lane);
+    wgt[tid] = wi;
+    __syncthreads();
+    const int cnt = min(kMergeThreads, n_sp - i0);
+#pragma unroll 4
+    for (int k = w; k < cnt; k += kMergeWaves) {
+      const float wk = wgt[k];
+      const float2 v = *reinterpret_cast<const float2*>(base + (int64_t)(i0 + k) * kPartStride +
+                                                        2 * lane);
       o0 += wk * v.x;
       o1 += wk * v.y;
     }
   }
   for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+  __syncthreads();
+  if (lane == 0) sred[w] = L;
+  red[w][2 * lane] = o0;
+  red[w][2 * lane + 1] = o1;
+  __syncthreads();
+  if (w != 0) return;
+  L = sred[0];
+  o0 = red[0][2 * lane];
+  o1 = red[0][2 * lane + 1];
+#pragma unroll
+  for (int i = 1; i < kMergeWaves; ++i) {
+    L += sred[i];
+    o0 += red[i][2 * lane];
+    o1 += red[i][2 * lane + 1];
+  }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   const int64_t row = ((int64_t)s * a.num_q_heads + qhd) * kD;
   if constexpr (OUT_DTYPE == AMF_DTYPE_F32) {
@@ -794,10 +822,10 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
   }
   dim3 mgrid((unsigned)num_q_heads, (unsigned)num_seqs);
   if (out_dtype == AMF_DTYPE_BF16)
-    int4_decode_merge_kernel<AMF_DTYPE_BF16><<<mgrid, 64, 0, st>>>(a);
+    int4_decode_merge_kernel<AMF_DTYPE_BF16><<<mgrid, kMergeThreads, 0, st>>>(a);
   else if (out_dtype == AMF_DTYPE_F16)
-    int4_decode_merge_kernel<AMF_DTYPE_F16><<<mgrid, 64, 0, st>>>(a);
+    int4_decode_merge_kernel<AMF_DTYPE_F16><<<mgrid, kMergeThreads, 0, st>>>(a);
   else
-    int4_decode_merge_kernel<AMF_DTYPE_F32><<<mgrid, 64, 0, st>>>(a);
+    int4_decode_merge_kernel<AMF_DTYPE_F32><<<mgrid, kMergeThreads, 0, st>>>(a);
   return check_launch(who);
 }

@@ -245,6 +245,21 @@ class DecodeCase:
 # -------------------------------------------------------------------- main --
 
 
+def profiled_traffic(name: str):
+    """HBM bytes per launch recorded by the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    runs of this workload (profiles/<name>.md, counters scaled by the
+    page-copy calibration), or None when no summary is present."""
+    path = os.path.join(ROOT, "profiles", name + ".md")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_threads() -> int:
     n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     return max(1, min(int(n or 1), 16))
@@ -278,16 +293,17 @@ def main() -> int:
     if args.profile:
         if args.profile == "copy":
             # Calibration for the HBM byte counters: a raw page copy of exactly
-            # 1 GiB read + 1 GiB written (1 plane of 32768 pages of 32 KiB).
+            # 1 GiB read + 1 GiB written (2 planes of 16384 pages of 32 KiB).
             from korith_vllm_ext import _paged
 
-            src = torch.empty(32768, 16, 8, 128, dtype=torch.bfloat16, device=DEV).fill_(1.0)
+            src = torch.empty(2, 16384, 16, 8, 128, dtype=torch.bfloat16, device=DEV).fill_(1.0)
             dst = torch.empty_like(src)
             view = _paged.cache_view([src])
-            fn = lambda: _paged.gather_pages(view, None, [dst.data_ptr(), dst.data_ptr()],
-                                             view.page_bytes, 32768)
+            fn = lambda: _paged.gather_pages(view, None, [dst[0].data_ptr(), dst[1].data_ptr()],
+                                             view.page_bytes, 16384)
             ms = time_launches(fn, args.steps, args.warmup)
-            log(f"copy: {ms:.4f} ms/launch, 2 GiB read + 2 GiB written per launch")
+            log(f"copy: {ms:.4f} ms/launch, 1 GiB read + 1 GiB written per launch, "
+                f"{2 * 2**30 / ms / 1e6:.1f} GB/s")
             return 0
         if args.profile in ("fp8_restore", "int4_restore"):
             fmt = "fp8_e4m3_ph" if args.profile == "fp8_restore" else "int4_asym_g32"
@@ -326,7 +342,8 @@ def main() -> int:
                    "format": "fp8_e4m3_ph", "cache_dtype": "bf16", "parallelism": "none"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "fp8_dequant_scatter_kernel",
+                     "traffic": profiled_traffic("fp8_dequant_scatter_llama3_8b_512p"),
+                     "kernel": "fp8_dequant_scatter_kernel",
                      "algo_bytes_per_launch": fp8.algo_bytes},
     }
     if not args.no_cpu_baseline:

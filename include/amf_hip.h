@@ -244,6 +244,27 @@ int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* out, int32_
                                void* workspace, int64_t workspace_bytes,
                                int32_t algo, int32_t* err_flag, void* stream);
 
+/* ---- dense attention ---------------------------------------------------------
+ * out = softmax(q k^T * softmax_scale + mask) v, per query row, computed in
+ * fp32 and rounded once to out_dtype.  q [batch, num_q_heads, q_len, head_dim],
+ * k and v [batch, num_kv_heads, kv_len, head_dim], out like q; all contiguous,
+ * q/k/v of one dtype (AMF_DTYPE_*).  num_q_heads must be a multiple of
+ * num_kv_heads (GQA; query head h reads KV head h / (num_q_heads/num_kv_heads)).
+ * mask: NULL or fp32 additive mask read at
+ *   b*mask_stride_b + h*mask_stride_h + i*mask_stride_q + t*mask_stride_t
+ * (element strides; 0 broadcasts).  kv_len 0 gives zeros; a row whose scores
+ * are all -inf gives NaN, as softmax does.  head_dim <= 256.
+ * Replaces the attention of fallback_fp16_kernel (kernels/dispatch.py:117-143),
+ * which int4_decode_attention (int4_decode_attention.py:6-9) reaches for k/v
+ * given as tensors or CompressedKV without a block table. */
+int amf_dense_attn(const void* q, const void* k, const void* v, int32_t dtype,
+                   const float* mask, int64_t mask_stride_b, int64_t mask_stride_h,
+                   int64_t mask_stride_q, int64_t mask_stride_t,
+                   void* out, int32_t out_dtype,
+                   int64_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                   int64_t q_len, int64_t kv_len, int32_t head_dim,
+                   float softmax_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

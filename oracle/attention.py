@@ -60,3 +60,30 @@ def fallback_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if mask is not None:
         attn = attn + mask
     return torch.matmul(torch.softmax(attn, dim=-1), v)
+
+
+def dense_attention_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray,
+                        scale: Optional[float] = None,
+                        mask: Optional[np.ndarray] = None) -> np.ndarray:
+    """softmax(q k^T * scale + mask) v in float64 (dispatch.py:117-143 math),
+    q [B, Hq, Tq, D], k/v [B, Hkv, T, D] with GQA (query head h reads KV head
+    h // (Hq / Hkv)), mask broadcastable to [B, Hq, Tq, T].  T == 0 gives
+    zeros (an empty sum); a row of all -inf scores gives NaN."""
+    B, Hq, Tq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    R = Hq // Hkv
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = np.zeros((B, Hq, Tq, D), dtype=np.float64)
+    if T == 0:
+        return out
+    kk = np.repeat(k.astype(np.float64), R, axis=1)
+    vv = np.repeat(v.astype(np.float64), R, axis=1)
+    s = np.einsum("bhqd,bhtd->bhqt", q.astype(np.float64), kk) * scale
+    if mask is not None:
+        s = s + np.broadcast_to(mask.astype(np.float64), s.shape)
+    with np.errstate(invalid="ignore"):
+        m = s.max(axis=-1, keepdims=True)
+        p = np.exp(s - m)
+        p = p / p.sum(axis=-1, keepdims=True)
+    return np.einsum("bhqt,bhtd->bhqd", p, vv)
