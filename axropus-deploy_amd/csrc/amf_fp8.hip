@@ -21,8 +21,8 @@ using namespace amf;
 constexpr int kThreads = 256;
 constexpr int kMaxRowsPerLane = 16;  // page rows a lane may keep in registers on save
 
-// bf16(1e-8) as fp32: the floor clamp_min_(1e-8) applies on a bf16 tensor
-// (amf_codec.py:183).  An fp16 tensor rounds 1e-8 to 0.
+// The floor clamp_min_(1e-8) applies in the tensor's own dtype
+// (amf_codec.py:183): bf16(1e-8) (these bits), fp16(1e-8) = 0, fp32(1e-8).
 constexpr uint32_t kBf16FloorBits = 0x322C0000u;
 constexpr float kFp8Max = 448.0f;
 
@@ -39,9 +39,20 @@ __device__ __forceinline__ int lane_col(const PageGeom& g) { return threadIdx.x 
 __device__ __forceinline__ int lane_row0(const PageGeom& g) { return threadIdx.x >> g.cpr_log2; }
 __device__ __forceinline__ int rows_per_iter(const PageGeom& g) { return kThreads >> g.cpr_log2; }
 
-template <bool BF16>
+template <int DT>
 __device__ __forceinline__ float tensor_floor() {
-  return BF16 ? u2f(kBf16FloorBits) : 0.0f;
+  if constexpr (DT == AMF_DTYPE_BF16) {
+    return u2f(kBf16FloorBits);
+  } else if constexpr (DT == AMF_DTYPE_F16) {
+    return 0.0f;
+  } else {
+    return 1e-8f;
+  }
+}
+
+template <bool BF16>
+constexpr int dtype_of() {
+  return BF16 ? AMF_DTYPE_BF16 : AMF_DTYPE_F16;
 }
 
 // ---------------------------------------------------------------- restore --
@@ -50,7 +61,7 @@ __device__ __forceinline__ float tensor_floor() {
 // cache elements out), so each wave-wide store covers 1 KiB contiguously and
 // every cache line is written whole.  The chunk's head is fixed per lane when
 // 2048 elements (one workgroup pass) span whole rows of heads.
-template <bool BF16, bool PER_TENSOR>
+template <int DT, bool PER_TENSOR>
 __global__ __launch_bounds__(kThreads) void fp8_dequant_scatter_kernel(
     const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
@@ -96,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void fp8_dequant_scatter_kernel(
         e4m3x4_to_f32(c[u][1], x + 4);
 #pragma unroll
         for (int q = 0; q < 8; ++q) x[q] = x[q] * s;
-        st_stream(pack8<BF16>(x), reinterpret_cast<u32x4*>(out) + k);
+        store8<DT>(out + (int64_t)k * (8 * elem_bytes<DT>()), x);
       }
     }
   }
@@ -107,7 +118,7 @@ __global__ __launch_bounds__(kThreads) void fp8_dequant_scatter_kernel(
 // Per-tensor absmax (first of the three per-tensor save kernels): a
 // workgroup's page max goes to its scale group's slot ws[plane / pps] by an
 // integer atomic max on the non-negative float's bit pattern.
-template <bool BF16>
+template <int DT>
 __global__ __launch_bounds__(kThreads) void fp8_absmax_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
     const int32_t* __restrict__ block_ids, int64_t pool, PageGeom g, uint32_t* ws,
@@ -124,10 +135,10 @@ __global__ __launch_bounds__(kThreads) void fp8_absmax_kernel(
   const int col = lane_col(g), rpi = rows_per_iter(g);
   float m = 0.0f;
   for (int r = lane_row0(g); r < g.n_rows; r += rpi) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(src + 2 * ((int64_t)r * g.head_dim + col * 16));
+    const uint8_t* p = src + elem_bytes<DT>() * ((int64_t)r * g.head_dim + col * 16);
     float x[16];
-    unpack8<BF16>(p[0], x);
-    unpack8<BF16>(p[1], x + 8);
+    load8<DT>(p, x);
+    load8<DT>(p + 8 * elem_bytes<DT>(), x + 8);
 #pragma unroll
     for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(x[q]));
   }
@@ -149,21 +160,21 @@ __global__ void fill_u32_kernel(uint32_t* p, int n, uint32_t v) {
 // amf_codec.py:182-191 computes it: absmax clamped to the dtype's 1e-8 floor,
 // divided by 448 (double division then rounding to fp32 equals one fp32
 // division since 53 >= 2*24 + 2).
-template <bool BF16>
+template <int DT>
 __device__ __forceinline__ float tensor_scale_from(uint32_t amax_bits) {
-  return fmaxf(u2f(amax_bits), tensor_floor<BF16>()) / kFp8Max;
+  return fmaxf(u2f(amax_bits), tensor_floor<DT>()) / kFp8Max;
 }
 
 // Writes each scale group's sidecar [k_scale, v_scale, q_scale, prob_scale]
 // = [s, s, 1, 1] (FP8ScaleSidecar(k_scale=scale, v_scale=scale),
 // amf_codec.py:200) from the first plane of the group.
-template <bool BF16>
+template <int DT>
 __global__ void fp8_tensor_finalize_kernel(const uint64_t* __restrict__ param_planes,
                                            const uint32_t* __restrict__ ws, int n_planes, int pps) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n_planes && i % pps == 0) {
     float* sc = reinterpret_cast<float*>(param_planes[i]);
-    const float s = tensor_scale_from<BF16>(ws[i / pps]);
+    const float s = tensor_scale_from<DT>(ws[i / pps]);
     sc[0] = s;
     sc[1] = s;
     sc[2] = 1.0f;
@@ -238,7 +249,7 @@ __global__ __launch_bounds__(kThreads) void fp8_quant_gather_kernel(
 
   float tdiv = 0.0f, trcp = 0.0f;
   if (PER_TENSOR) {
-    const float a = fmaxf(u2f(ws[plane / g.pps]), tensor_floor<BF16>());
+    const float a = fmaxf(u2f(ws[plane / g.pps]), tensor_floor<dtype_of<BF16>()>());
     // amf_codec.py:191 divides by max(scale, 1e-12); only a zero absmax (an
     // fp16 cache, whose floor rounds to 0) reaches that clamp.
     tdiv = (a == 0.0f) ? 1e-12f : a / kFp8Max;
@@ -265,6 +276,70 @@ __global__ __launch_bounds__(kThreads) void fp8_quant_gather_kernel(
       st_stream(
           c, reinterpret_cast<u32x4*>(codes + (int64_t)row * g.head_dim + col * 16));
     }
+  }
+}
+
+// Save of pages larger than the register-resident kernel holds, and of fp32
+// caches: the page is read twice (per-(page, head) absmax, then codes; the
+// second read hits in cache).  One lane = one 8-element chunk per step;
+// head_dim % 16 == 0, so a chunk never straddles rows.  Same arithmetic as
+// fp8_quant_gather_kernel.
+template <int DT, bool PER_TENSOR>
+__global__ __launch_bounds__(kThreads) void fp8_quant_gather_looped_kernel(
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
+    const uint64_t* __restrict__ param_planes, PageGeom g, const uint32_t* __restrict__ ws,
+    int32_t* err_flag) {
+  constexpr int ES = elem_bytes<DT>();
+  const int64_t j = blockIdx.x;
+  const int plane = blockIdx.y;
+  const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
+  __shared__ uint32_t s_amax[kThreads];
+  if (sp < 0 || sp >= pool) {
+    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    return;
+  }
+  const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
+  const int64_t n8 = page_elems >> 3;
+  const uint8_t* __restrict__ src =
+      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
+  uint8_t* __restrict__ codes = reinterpret_cast<uint8_t*>(code_planes[plane]) + j * page_elems;
+  float* __restrict__ params = reinterpret_cast<float*>(param_planes[plane]);
+  if (!PER_TENSOR) {
+    for (int h = threadIdx.x; h < g.num_heads; h += kThreads) s_amax[h] = 0;
+    __syncthreads();
+    for (int64_t k = threadIdx.x; k < n8; k += kThreads) {
+      float x[8];
+      load8<DT>(src + k * (8 * ES), x);
+      float m = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[q]));
+      atomicMax(&s_amax[(int)((k * 8 / g.head_dim) % g.num_heads)], f2u(m));
+    }
+    __syncthreads();
+    for (int h = threadIdx.x; h < g.num_heads; h += kThreads)
+      params[j * g.num_heads + h] = fmaxf(u2f(s_amax[h]), 1e-8f) / kFp8Max;
+  }
+  float tdiv = 0.0f, trcp = 0.0f;
+  if (PER_TENSOR) {
+    const float a = fmaxf(u2f(ws[plane / g.pps]), tensor_floor<DT>());
+    tdiv = (a == 0.0f) ? 1e-12f : a / kFp8Max;
+    trcp = 1.0f / tdiv;
+  }
+  for (int64_t k = threadIdx.x; k < n8; k += kThreads) {
+    float b = tdiv, rb = trcp;
+    if (!PER_TENSOR) {
+      b = fmaxf(u2f(s_amax[(int)((k * 8 / g.head_dim) % g.num_heads)]), 1e-8f) / kFp8Max;
+      rb = 1.0f / b;
+    }
+    float x[8];
+    load8<DT>(src + k * (8 * ES), x);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) x[q] = fminf(fmaxf(div_rn(x[q], b, rb), -kFp8Max), kFp8Max);
+    u32x2 c;
+    c[0] = f32x4_to_e4m3(x);
+    c[1] = f32x4_to_e4m3(x + 4);
+    st_stream(c, reinterpret_cast<u32x2*>(codes) + k);
   }
 }
 
@@ -307,16 +382,12 @@ extern "C" int amf_fp8_dequant_scatter(int32_t format, const uint64_t* code_plan
   if (n_pages == 0) return ok();
   dim3 grid((unsigned)n_pages, (unsigned)n_planes);
   hipStream_t s = as_stream(stream);
-  const bool bf16 = cache_dtype == AMF_DTYPE_BF16;
   const bool pt = format == AMF_FMT_FP8_E4M3;
-#define AMF_LAUNCH(B, T)                                                                   \
-  fp8_dequant_scatter_kernel<B, T><<<grid, kThreads, 0, s>>>(                              \
+#define AMF_LAUNCH(T)                                                                      \
+  fp8_dequant_scatter_kernel<DT, T><<<grid, kThreads, 0, s>>>(                             \
       code_planes, param_planes, cache_planes, cache_page_stride, block_ids, pool_pages, g, \
       err_flag)
-  if (bf16 && pt) AMF_LAUNCH(true, true);
-  else if (bf16) AMF_LAUNCH(true, false);
-  else if (pt) AMF_LAUNCH(false, true);
-  else AMF_LAUNCH(false, false);
+  AMF_WITH_DTYPE(cache_dtype, if (pt) AMF_LAUNCH(true); else AMF_LAUNCH(false));
 #undef AMF_LAUNCH
   return check_launch(who);
 }
@@ -343,9 +414,9 @@ extern "C" int amf_fp8_quant_gather(int32_t format, const uint64_t* cache_planes
   PageGeom g;
   if ((rc = make_geom(who, block_size, num_heads, head_dim, planes_per_scale, &g))) return rc;
   const int rpi = kThreads >> g.cpr_log2;
-  if (g.n_rows > rpi * kMaxRowsPerLane)
-    return fail(AMF_ERR_UNSUPPORTED, "%s: page of %d rows exceeds %d", who, g.n_rows,
-                rpi * kMaxRowsPerLane);
+  // Pages that fit lanes' registers take the single-read kernel; larger pages
+  // and fp32 caches the two-read one.
+  const bool looped = cache_dtype == AMF_DTYPE_F32 || g.n_rows > rpi * kMaxRowsPerLane;
   if (format == AMF_FMT_FP8_E4M3_PH && num_heads > kThreads)
     return fail(AMF_ERR_UNSUPPORTED, "%s: num_heads > %d", who, kThreads);
   const int64_t need = amf_quant_workspace_bytes(format, n_planes, planes_per_scale, head_dim);
@@ -354,44 +425,45 @@ extern "C" int amf_fp8_quant_gather(int32_t format, const uint64_t* cache_planes
                 (long long)need);
   if (n_pages == 0) return ok();
   hipStream_t s = as_stream(stream);
-  const bool bf16 = cache_dtype == AMF_DTYPE_BF16;
   dim3 grid((unsigned)n_pages, (unsigned)n_planes);
   uint32_t* ws = reinterpret_cast<uint32_t*>(workspace);
   const int n_groups = n_planes / g.pps;
   if (pt) {
     fill_u32_kernel<<<(n_groups + 255) / 256, 256, 0, s>>>(ws, n_groups, 0u);
-    if (bf16)
-      fp8_absmax_kernel<true><<<grid, kThreads, 0, s>>>(cache_planes, cache_page_stride,
-                                                        block_ids, pool_pages, g, ws, err_flag);
-    else
-      fp8_absmax_kernel<false><<<grid, kThreads, 0, s>>>(cache_planes, cache_page_stride,
-                                                         block_ids, pool_pages, g, ws, err_flag);
+    AMF_WITH_DTYPE(cache_dtype,
+                   fp8_absmax_kernel<DT><<<grid, kThreads, 0, s>>>(
+                       cache_planes, cache_page_stride, block_ids, pool_pages, g, ws, err_flag));
   }
-  const int rows = (g.n_rows + rpi - 1) / rpi;
+  if (looped) {
+#define AMF_LAUNCH(T)                                                                         \
+  fp8_quant_gather_looped_kernel<DT, T><<<grid, kThreads, 0, s>>>(                            \
+      cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, param_planes, g, ws, \
+      err_flag)
+    AMF_WITH_DTYPE(cache_dtype, if (pt) AMF_LAUNCH(true); else AMF_LAUNCH(false));
+#undef AMF_LAUNCH
+  } else {
+    const int rows = (g.n_rows + rpi - 1) / rpi;
+    const bool bf16 = cache_dtype == AMF_DTYPE_BF16;
 #define AMF_LAUNCH(B, T, R)                                                                   \
   fp8_quant_gather_kernel<B, T, R><<<grid, kThreads, 0, s>>>(cache_planes, cache_page_stride,  \
                                                              block_ids, pool_pages,            \
                                                              code_planes, param_planes, g, ws, \
                                                              err_flag)
-#define AMF_LAUNCH_R(B, T)              \
-  if (rows <= 1) AMF_LAUNCH(B, T, 1);   \
+#define AMF_LAUNCH_R(B, T)                 \
+  if (rows <= 1) AMF_LAUNCH(B, T, 1);      \
   else if (rows <= 2) AMF_LAUNCH(B, T, 2); \
   else if (rows <= 4) AMF_LAUNCH(B, T, 4); \
   else if (rows <= 8) AMF_LAUNCH(B, T, 8); \
   else AMF_LAUNCH(B, T, 16)
-  if (bf16 && pt) { AMF_LAUNCH_R(true, true); }
-  else if (bf16) { AMF_LAUNCH_R(true, false); }
-  else if (pt) { AMF_LAUNCH_R(false, true); }
-  else { AMF_LAUNCH_R(false, false); }
+    if (bf16 && pt) { AMF_LAUNCH_R(true, true); }
+    else if (bf16) { AMF_LAUNCH_R(true, false); }
+    else if (pt) { AMF_LAUNCH_R(false, true); }
+    else { AMF_LAUNCH_R(false, false); }
 #undef AMF_LAUNCH_R
 #undef AMF_LAUNCH
-  if (pt) {
-    if (bf16)
-      fp8_tensor_finalize_kernel<true><<<(n_planes + 255) / 256, 256, 0, s>>>(param_planes, ws,
-                                                                              n_planes, g.pps);
-    else
-      fp8_tensor_finalize_kernel<false><<<(n_planes + 255) / 256, 256, 0, s>>>(param_planes, ws,
-                                                                               n_planes, g.pps);
   }
+  if (pt)
+    AMF_WITH_DTYPE(cache_dtype, fp8_tensor_finalize_kernel<DT>
+                   <<<(n_planes + 255) / 256, 256, 0, s>>>(param_planes, ws, n_planes, g.pps));
   return check_launch(who);
 }

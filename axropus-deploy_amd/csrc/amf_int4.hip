@@ -40,26 +40,18 @@ __device__ __forceinline__ int sym_col(const SymGeom& g) { return threadIdx.x & 
 __device__ __forceinline__ int sym_row0(const SymGeom& g) { return threadIdx.x >> g.cpr_log2; }
 __device__ __forceinline__ int sym_rpi(const SymGeom& g) { return kThreads >> g.cpr_log2; }
 
-// 32 cache elements (64 bytes) at `p` -> fp32.
-template <bool BF16>
+// 32 cache elements at byte address `p` -> fp32.
+template <int DT>
 __device__ __forceinline__ void load32(const uint8_t* p, float* x) {
-  const u32x4* v = reinterpret_cast<const u32x4*>(p);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) unpack8<BF16>(v[q], x + 8 * q);
-}
-
-template <bool BF16>
-__device__ __forceinline__ void store32(uint8_t* p, const float* x) {
-  u32x4* v = reinterpret_cast<u32x4*>(p);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) st_stream(pack8<BF16>(x + 8 * q), v + q);
+  for (int q = 0; q < 4; ++q) load8<DT>(p + q * (8 * elem_bytes<DT>()), x + 8 * q);
 }
 
 // CHANNEL = false: INT4_SYM_BLOCK (params: [n_pages] fp16);
 // CHANNEL = true : INT4_SYM       (params: [head_dim] fp16 per scale group).
 // One lane = one 8-element chunk (4 code bytes in, one 16-byte vector out):
 // wave-wide stores cover 1 KiB contiguously.
-template <bool BF16, bool CHANNEL>
+template <int DT, bool CHANNEL>
 __global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
     const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
@@ -102,7 +94,7 @@ __global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
         float x[8];
 #pragma unroll
         for (int n = 0; n < 8; ++n) x[n] = (nib(c[u], n) - 8.0f) * (CHANNEL ? s_ch[n] : s_page);
-        st_stream(pack8<BF16>(x), reinterpret_cast<u32x4*>(out) + k);
+        store8<DT>(out + (int64_t)k * (8 * elem_bytes<DT>()), x);
       }
     }
   }
@@ -183,10 +175,63 @@ __global__ __launch_bounds__(kThreads) void int4_symblock_quant_gather_kernel(
   }
 }
 
+// INT4_SYM_BLOCK save of pages larger than the register-resident kernel
+// holds, and of fp32 caches: the page absmax in a first read, the codes in a
+// second (which hits in cache).  One lane = one 8-element chunk per step.
+// Same arithmetic as int4_symblock_quant_gather_kernel.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void int4_symblock_quant_looped_kernel(
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
+    const uint64_t* __restrict__ param_planes, SymGeom g, int32_t* err_flag) {
+  constexpr int ES = elem_bytes<DT>();
+  const int64_t j = blockIdx.x;
+  const int plane = blockIdx.y;
+  const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
+  if (sp < 0 || sp >= pool) {
+    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    return;
+  }
+  const int64_t n8 = (int64_t)g.n_rows * g.head_dim / 8;
+  const uint8_t* __restrict__ src =
+      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
+  uint32_t* __restrict__ codes = reinterpret_cast<uint32_t*>(code_planes[plane]) + j * n8;
+  _Float16* __restrict__ params = reinterpret_cast<_Float16*>(param_planes[plane]);
+  float m = 0.0f;
+  for (int64_t k = threadIdx.x; k < n8; k += kThreads) {
+    float x[8];
+    load8<DT>(src + k * (8 * ES), x);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) m = fmaxf(m, fabsf(x[n]));
+  }
+  m = wave_max_xor(m, 64);
+  __shared__ float s_wmax[kThreads / 64];
+  if ((threadIdx.x & 63) == 0) s_wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float amax = s_wmax[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) amax = fmaxf(amax, s_wmax[w]);
+  const float scale = fmaxf(amax, 1e-8f) / kSymMax;
+  const float rscale = 1.0f / scale;
+  if (threadIdx.x == 0) params[j] = (_Float16)scale;
+  for (int64_t k = threadIdx.x; k < n8; k += kThreads) {
+    float x[8];
+    load8<DT>(src + k * (8 * ES), x);
+    uint32_t w = 0;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      float qv = __builtin_rintf(div_rn(x[n], scale, rscale));
+      qv = fminf(fmaxf(qv, -8.0f), 7.0f);
+      w |= (uint32_t)((int)qv + 8) << (4 * n);
+    }
+    st_stream(w, codes + k);
+  }
+}
+
 // INT4_SYM save, pass 1: per-channel absmax over a scale group.  Each
 // workgroup folds a strided set of pages into an LDS table, then issues one
 // global atomic max per channel into ws[group][head_dim].
-template <bool BF16>
+template <int DT>
 __global__ __launch_bounds__(kThreads) void int4_channel_absmax_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
     const int32_t* __restrict__ block_ids, int64_t pool, int64_t n_pages, SymGeom g,
@@ -208,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void int4_channel_absmax_kernel(
     const uint8_t* src = reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
     for (int r = sym_row0(g); r < g.n_rows; r += rpi) {
       float x[32];
-      load32<BF16>(src + 2 * ((int64_t)r * g.head_dim + col * 32), x);
+      load32<DT>(src + elem_bytes<DT>() * ((int64_t)r * g.head_dim + col * 32), x);
 #pragma unroll
       for (int q = 0; q < 32; ++q) m[q] = fmaxf(m[q], fabsf(x[q]));
     }
@@ -225,7 +270,7 @@ __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
   if (i < n) p[i] = v;
 }
 
-template <bool BF16>
+template <int DT>
 __global__ __launch_bounds__(kThreads) void int4_channel_quant_gather_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
     const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
@@ -251,7 +296,7 @@ __global__ __launch_bounds__(kThreads) void int4_channel_quant_gather_kernel(
   }
   for (int r = sym_row0(g); r < g.n_rows; r += rpi) {
     float x[32];
-    load32<BF16>(src + 2 * ((int64_t)r * g.head_dim + col * 32), x);
+    load32<DT>(src + elem_bytes<DT>() * ((int64_t)r * g.head_dim + col * 32), x);
     u32x4 c;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -337,7 +382,7 @@ __device__ __forceinline__ float param_zero(uint32_t w) {
 //  K: (head, token, group): 16 code bytes + 1 param word -> 32 outputs of a row
 //  V: (head, 8-dim block, token half): 32 code bytes + 8 param words ->
 //     8 tokens x 8 dims.
-template <bool BF16>
+template <int DT>
 __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
     const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
@@ -374,7 +419,7 @@ __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
       float x[8];
 #pragma unroll
       for (int n = 0; n < 8; ++n) x[n] = nib(c, n) * s + z;
-      st_stream(pack8<BF16>(x), reinterpret_cast<u32x4*>(out) + it);
+      store8<DT>(out + (int64_t)it * (8 * elem_bytes<DT>()), x);
     }
   } else {
     const int nb = D / 8;
@@ -399,9 +444,7 @@ __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
 #pragma unroll
         for (int k = 0; k < 8; ++k) x[k] = nib(w[k], i) * s + z;
         const int t = 8 * th + i;
-        st_stream(
-            pack8<BF16>(x),
-            reinterpret_cast<u32x4*>(out + 2 * ((int64_t)(t * H + h) * D + 8 * b)));
+        store8<DT>(out + elem_bytes<DT>() * ((int64_t)(t * H + h) * D + 8 * b), x);
       }
     }
   }
@@ -409,7 +452,7 @@ __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
 
 // Save of one page of a K plane: items (head, token, group) read 64 cache
 // bytes, write 16 code bytes and one param word.
-template <bool BF16>
+template <int DT>
 __device__ __forceinline__ void asym_quant_k(const uint8_t* __restrict__ src,
                                              uint8_t* __restrict__ codes,
                                              uint32_t* __restrict__ params, const AsymGeom& g) {
@@ -421,7 +464,7 @@ __device__ __forceinline__ void asym_quant_k(const uint8_t* __restrict__ src,
     const int th = it / G;  // token * H + head
     const int t = th / H, h = th % H;
     float x[32];
-    load32<BF16>(src + 2 * ((int64_t)th * D + 32 * gi), x);
+    load32<DT>(src + elem_bytes<DT>() * ((int64_t)th * D + 32 * gi), x);
     const AsymParams p = asym_params(x);
     u32x4 c;
 #pragma unroll
@@ -439,20 +482,26 @@ __device__ __forceinline__ void asym_quant_k(const uint8_t* __restrict__ src,
 }
 
 // Save of one page of a V plane.  Groups run along head_dim while the code
-// tiles run along tokens, so the page is staged in LDS: phase 1 computes every
-// group's (mn, scale), phase 2 builds the 8-token x 8-dim tiles.
+// tiles run along tokens: phase 1 computes every group's (mn, scale) into LDS
+// tables, phase 2 builds the 8-token x 8-dim tiles.  STAGED copies the page
+// into LDS first (when it fits); otherwise both phases read the page from
+// global memory, where the second read hits in cache.
 constexpr int kAsymLdsBytes = 64 * 1024;
 
-template <bool BF16>
+template <int DT, bool STAGED>
 __device__ __forceinline__ void asym_quant_v(const uint8_t* __restrict__ src,
                                              uint8_t* __restrict__ codes,
                                              uint32_t* __restrict__ params, const AsymGeom& g,
                                              uint8_t* lds) {
+  constexpr int ES = elem_bytes<DT>();
   const int H = g.num_heads, D = g.head_dim, G = g.groups;
-  const int page_bytes = 16 * H * D * 2;
+  const int page_bytes = STAGED ? 16 * H * D * ES : 0;
   // phase 0: page -> LDS (cache layout)
-  for (int o = threadIdx.x * 16; o < page_bytes; o += kThreads * 16)
-    *reinterpret_cast<u32x4*>(lds + o) = *reinterpret_cast<const u32x4*>(src + o);
+  if (STAGED) {
+    for (int o = threadIdx.x * 16; o < page_bytes; o += kThreads * 16)
+      *reinterpret_cast<u32x4*>(lds + o) = *reinterpret_cast<const u32x4*>(src + o);
+  }
+  const uint8_t* data = STAGED ? lds : src;
   float* s_mn = reinterpret_cast<float*>(lds + page_bytes);          // [H][G][16]
   float* s_sc = s_mn + 16 * H * G;                                   // [H][G][16]
   float* s_rc = s_sc + 16 * H * G;                                   // [H][G][16]
@@ -464,9 +513,7 @@ __device__ __forceinline__ void asym_quant_v(const uint8_t* __restrict__ src,
     const int hg = it >> 4;
     const int h = hg / G, gi = hg % G;
     float x[32];
-    const u32x4* v = reinterpret_cast<const u32x4*>(lds + 2 * ((t * H + h) * D + 32 * gi));
-#pragma unroll
-    for (int q = 0; q < 4; ++q) unpack8<BF16>(v[q], x + 8 * q);
+    load32<DT>(data + ES * ((t * H + h) * D + 32 * gi), x);
     const AsymParams p = asym_params(x);
     s_mn[it] = p.mn;
     s_sc[it] = p.scale;
@@ -490,7 +537,7 @@ __device__ __forceinline__ void asym_quant_v(const uint8_t* __restrict__ src,
       p.scale = s_sc[pi];
       p.rscale = s_rc[pi];
       float x[8];
-      unpack8<BF16>(*reinterpret_cast<const u32x4*>(lds + 2 * ((t * H + h) * D + 8 * b)), x);
+      load8<DT>(data + ES * ((t * H + h) * D + 8 * b), x);
 #pragma unroll
       for (int k = 0; k < 8; ++k) w[k] |= asym_code(x[k], p) << (4 * i);
     }
@@ -500,7 +547,7 @@ __device__ __forceinline__ void asym_quant_v(const uint8_t* __restrict__ src,
   }
 }
 
-template <bool BF16>
+template <int DT, bool STAGED>
 __global__ __launch_bounds__(kThreads) void int4_asym_quant_gather_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
     const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
@@ -521,9 +568,9 @@ __global__ __launch_bounds__(kThreads) void int4_asym_quant_gather_kernel(
   uint32_t* __restrict__ params =
       reinterpret_cast<uint32_t*>(param_planes[plane]) + j * (int64_t)H * g.hb_param_words;
   if ((plane & 1) == 0)
-    asym_quant_k<BF16>(src, codes, params, g);
+    asym_quant_k<DT>(src, codes, params, g);
   else
-    asym_quant_v<BF16>(src, codes, params, g, lds);
+    asym_quant_v<DT, STAGED>(src, codes, params, g, lds);
 }
 
 int check_int4_format(const char* who, int32_t format) {
@@ -546,8 +593,11 @@ int make_sym_geom(const char* who, int32_t block_size, int32_t num_heads, int32_
   return ok();
 }
 
+// lds_staged: LDS of the V save with the page staged (the page in the cache
+// dtype + three fp32 tables of 16*H*G entries); lds_tables: the tables alone.
 int make_asym_geom(const char* who, int32_t block_size, int32_t num_heads, int32_t head_dim,
-                   int32_t n_planes, AsymGeom* g, size_t* lds_bytes) {
+                   int32_t elem_size, int32_t n_planes, AsymGeom* g, size_t* lds_staged,
+                   size_t* lds_tables) {
   if (block_size != 16)
     return fail(AMF_ERR_UNSUPPORTED, "%s: INT4_ASYM_G32 needs block_size 16 (got %d)", who,
                 block_size);
@@ -558,10 +608,10 @@ int make_asym_geom(const char* who, int32_t block_size, int32_t num_heads, int32
   g->groups = head_dim / 32;
   g->hb_code_bytes = 16 * head_dim / 2;
   g->hb_param_words = 16 * g->groups;
-  // LDS of the V save: the page (bf16) + three fp32 tables of 16*H*G entries.
-  *lds_bytes = (size_t)16 * num_heads * head_dim * 2 + (size_t)3 * 4 * 16 * num_heads * g->groups;
-  if (*lds_bytes > (size_t)kAsymLdsBytes)
-    return fail(AMF_ERR_UNSUPPORTED, "%s: page of %d heads x %d dims exceeds the LDS stage", who,
+  *lds_tables = (size_t)3 * 4 * 16 * num_heads * g->groups;
+  *lds_staged = (size_t)16 * num_heads * head_dim * elem_size + *lds_tables;
+  if (*lds_tables > (size_t)kAsymLdsBytes)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: %d heads x %d dims exceed the LDS parameter tables", who,
                 num_heads, head_dim);
   return ok();
 }
@@ -582,21 +632,18 @@ extern "C" int amf_int4_dequant_scatter(int32_t format, const uint64_t* code_pla
                             pool_pages, code_planes, param_planes, n_planes, n_pages, block_size,
                             num_heads, head_dim);
   if (rc) return rc;
-  const bool bf16 = cache_dtype == AMF_DTYPE_BF16;
   hipStream_t s = as_stream(stream);
   dim3 grid((unsigned)n_pages, (unsigned)n_planes);
   if (format == AMF_FMT_INT4_ASYM_G32) {
     AsymGeom g;
-    size_t lds;
-    if ((rc = make_asym_geom(who, block_size, num_heads, head_dim, n_planes, &g, &lds))) return rc;
+    size_t lds_staged, lds_tables;
+    if ((rc = make_asym_geom(who, block_size, num_heads, head_dim, cache_elem_bytes(cache_dtype),
+                             n_planes, &g, &lds_staged, &lds_tables)))
+      return rc;
     if (n_pages == 0) return ok();
-#define AMF_LAUNCH(B)                                                                           \
-  int4_asym_dequant_scatter_kernel<B><<<grid, kThreads, 0, s>>>(                                \
-      code_planes, param_planes, cache_planes, cache_page_stride, block_ids, pool_pages, g, \
-      err_flag)
-    if (bf16) AMF_LAUNCH(true);
-    else AMF_LAUNCH(false);
-#undef AMF_LAUNCH
+    AMF_WITH_DTYPE(cache_dtype, int4_asym_dequant_scatter_kernel<DT><<<grid, kThreads, 0, s>>>(
+                                    code_planes, param_planes, cache_planes, cache_page_stride,
+                                    block_ids, pool_pages, g, err_flag));
     return check_launch(who);
   }
   SymGeom g;
@@ -605,14 +652,11 @@ extern "C" int amf_int4_dequant_scatter(int32_t format, const uint64_t* code_pla
   if (ch && (8 * kThreads) % head_dim != 0)
     return fail(AMF_ERR_UNSUPPORTED, "%s: head_dim %d must divide %d", who, head_dim, 8 * kThreads);
   if (n_pages == 0) return ok();
-#define AMF_LAUNCH(B, C)                                                                        \
-  int4_sym_dequant_scatter_kernel<B, C><<<grid, kThreads, 0, s>>>(                              \
+#define AMF_LAUNCH(C)                                                                           \
+  int4_sym_dequant_scatter_kernel<DT, C><<<grid, kThreads, 0, s>>>(                             \
       code_planes, param_planes, cache_planes, cache_page_stride, block_ids, pool_pages, g, \
       err_flag)
-  if (bf16 && ch) AMF_LAUNCH(true, true);
-  else if (bf16) AMF_LAUNCH(true, false);
-  else if (ch) AMF_LAUNCH(false, true);
-  else AMF_LAUNCH(false, false);
+  AMF_WITH_DTYPE(cache_dtype, if (ch) AMF_LAUNCH(true); else AMF_LAUNCH(false));
 #undef AMF_LAUNCH
   return check_launch(who);
 }
@@ -637,17 +681,18 @@ extern "C" int amf_int4_quant_gather(int32_t format, const uint64_t* cache_plane
   dim3 grid((unsigned)n_pages, (unsigned)n_planes);
   if (format == AMF_FMT_INT4_ASYM_G32) {
     AsymGeom g;
-    size_t lds;
-    if ((rc = make_asym_geom(who, block_size, num_heads, head_dim, n_planes, &g, &lds))) return rc;
+    size_t lds_staged, lds_tables;
+    if ((rc = make_asym_geom(who, block_size, num_heads, head_dim, cache_elem_bytes(cache_dtype),
+                             n_planes, &g, &lds_staged, &lds_tables)))
+      return rc;
     if (n_pages == 0) return ok();
-    if (bf16)
-      int4_asym_quant_gather_kernel<true><<<grid, kThreads, lds, s>>>(
-          cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, param_planes, g,
-          err_flag);
-    else
-      int4_asym_quant_gather_kernel<false><<<grid, kThreads, lds, s>>>(
-          cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, param_planes, g,
-          err_flag);
+    const bool staged = lds_staged <= (size_t)kAsymLdsBytes;
+#define AMF_LAUNCH(ST)                                                                         \
+  int4_asym_quant_gather_kernel<DT, ST><<<grid, kThreads, ST ? lds_staged : lds_tables, s>>>(  \
+      cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, param_planes, g, \
+      err_flag)
+    AMF_WITH_DTYPE(cache_dtype, if (staged) AMF_LAUNCH(true); else AMF_LAUNCH(false));
+#undef AMF_LAUNCH
     return check_launch(who);
   }
   if (format == AMF_FMT_INT4_SYM &&
@@ -660,8 +705,14 @@ extern "C" int amf_int4_quant_gather(int32_t format, const uint64_t* cache_plane
   if (format == AMF_FMT_INT4_SYM_BLOCK) {
     const int rpi = kThreads >> g.cpr_log2;
     const int rows = (g.n_rows + rpi - 1) / rpi;
-    if (rows > 8)
-      return fail(AMF_ERR_UNSUPPORTED, "%s: page of %d rows exceeds %d", who, g.n_rows, 8 * rpi);
+    // Pages that fit lanes' registers take the single-read kernel; larger
+    // pages and fp32 caches the two-read one.
+    if (rows > 8 || cache_dtype == AMF_DTYPE_F32) {
+      AMF_WITH_DTYPE(cache_dtype, int4_symblock_quant_looped_kernel<DT><<<grid, kThreads, 0, s>>>(
+                                      cache_planes, cache_page_stride, block_ids, pool_pages,
+                                      code_planes, param_planes, g, err_flag));
+      return check_launch(who);
+    }
 #define AMF_LAUNCH(B, R)                                                                        \
   int4_symblock_quant_gather_kernel<B, R><<<grid, kThreads, 0, s>>>(                            \
       cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, param_planes, g, \
@@ -685,18 +736,12 @@ extern "C" int amf_int4_quant_gather(int32_t format, const uint64_t* cache_plane
   const int64_t n_ws = need / 4;
   fill_u32_kernel<<<(unsigned)((n_ws + 255) / 256), 256, 0, s>>>(ws, n_ws, 0u);
   dim3 rgrid((unsigned)(n_pages < 64 ? n_pages : 64), (unsigned)n_planes);
-  if (bf16)
-    int4_channel_absmax_kernel<true><<<rgrid, kThreads, 0, s>>>(
-        cache_planes, cache_page_stride, block_ids, pool_pages, n_pages, g, ws, err_flag);
-  else
-    int4_channel_absmax_kernel<false><<<rgrid, kThreads, 0, s>>>(
-        cache_planes, cache_page_stride, block_ids, pool_pages, n_pages, g, ws, err_flag);
-  if (bf16)
-    int4_channel_quant_gather_kernel<true><<<grid, kThreads, 0, s>>>(
-        cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, g, ws, err_flag);
-  else
-    int4_channel_quant_gather_kernel<false><<<grid, kThreads, 0, s>>>(
-        cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, g, ws, err_flag);
+  AMF_WITH_DTYPE(cache_dtype, int4_channel_absmax_kernel<DT><<<rgrid, kThreads, 0, s>>>(
+                                  cache_planes, cache_page_stride, block_ids, pool_pages, n_pages,
+                                  g, ws, err_flag));
+  AMF_WITH_DTYPE(cache_dtype, int4_channel_quant_gather_kernel<DT><<<grid, kThreads, 0, s>>>(
+                                  cache_planes, cache_page_stride, block_ids, pool_pages,
+                                  code_planes, g, ws, err_flag));
   dim3 fgrid((unsigned)((head_dim + 255) / 256), (unsigned)n_planes);
   int4_channel_finalize_kernel<<<fgrid, 256, 0, s>>>(param_planes, ws, n_planes, g.pps, head_dim);
   return check_launch(who);

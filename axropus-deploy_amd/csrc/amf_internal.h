@@ -24,10 +24,27 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 inline bool aligned16(int64_t v) { return (v & 15) == 0; }
 
 // Cache element size in bytes for an AMF_DTYPE_* tag; 0 if not a cache dtype
-// the codecs accept (bf16 and fp16).
+// the codecs accept (bf16, fp16, fp32).
 inline int cache_elem_bytes(int32_t dtype) {
-  return (dtype == AMF_DTYPE_BF16 || dtype == AMF_DTYPE_F16) ? 2 : 0;
+  if (dtype == AMF_DTYPE_BF16 || dtype == AMF_DTYPE_F16) return 2;
+  return dtype == AMF_DTYPE_F32 ? 4 : 0;
 }
+
+// Runs the statements after `dt` with `constexpr int DT` bound to the cache
+// dtype tag `dt` (validated beforehand by check_codec_geometry).
+#define AMF_WITH_DTYPE(dt, ...)                                       \
+  do {                                                                \
+    if ((dt) == AMF_DTYPE_BF16) {                                     \
+      constexpr int DT = AMF_DTYPE_BF16;                              \
+      __VA_ARGS__;                                                    \
+    } else if ((dt) == AMF_DTYPE_F16) {                               \
+      constexpr int DT = AMF_DTYPE_F16;                               \
+      __VA_ARGS__;                                                    \
+    } else {                                                          \
+      constexpr int DT = AMF_DTYPE_F32;                               \
+      __VA_ARGS__;                                                    \
+    }                                                                 \
+  } while (0)
 
 // Common validation of the paged-geometry arguments of the codec entry points.
 int check_codec_geometry(const char* who, const uint64_t* cache_planes,

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/amf_hip.h"
 #include "amf_device.h"
 
 namespace amf {
@@ -105,6 +106,43 @@ __device__ __forceinline__ u32x4 pack8(const float* x) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) r[i] = pack2<BF16>(x[2 * i], x[2 * i + 1]);
   return r;
+}
+
+// ---- cache elements of any AMF_DTYPE_* tag ----------------------------------
+
+// Bytes per element of a cache dtype tag.
+template <int DT>
+__host__ __device__ constexpr int elem_bytes() {
+  return DT == AMF_DTYPE_F32 ? 4 : 2;
+}
+
+// Eight consecutive cache elements at byte address p (aligned to 8 elements)
+// -> fp32: one 16-byte vector for bf16/fp16, two for fp32.
+template <int DT>
+__device__ __forceinline__ void load8(const uint8_t* p, float* x) {
+  if constexpr (DT == AMF_DTYPE_F32) {
+    const f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
+    const f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = a[i];
+      x[4 + i] = b[i];
+    }
+  } else {
+    unpack8<DT == AMF_DTYPE_BF16>(*reinterpret_cast<const u32x4*>(p), x);
+  }
+}
+
+// fp32 -> eight cache elements at byte address p (streaming store; bf16/fp16
+// round to nearest even).
+template <int DT>
+__device__ __forceinline__ void store8(uint8_t* p, const float* x) {
+  if constexpr (DT == AMF_DTYPE_F32) {
+    st_stream(f32x4{x[0], x[1], x[2], x[3]}, reinterpret_cast<f32x4*>(p));
+    st_stream(f32x4{x[4], x[5], x[6], x[7]}, reinterpret_cast<f32x4*>(p) + 1);
+  } else {
+    st_stream(pack8<DT == AMF_DTYPE_BF16>(x), reinterpret_cast<u32x4*>(p));
+  }
 }
 
 // ---- fp8 e4m3fn -------------------------------------------------------------

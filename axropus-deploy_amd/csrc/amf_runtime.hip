@@ -44,14 +44,15 @@ int check_codec_geometry(const char* who, const uint64_t* cache_planes,
   if (block_size <= 0 || num_heads <= 0 || head_dim <= 0)
     return fail(AMF_ERR_INVALID_ARG, "%s: bad geometry bs=%d H=%d D=%d", who, block_size,
                 num_heads, head_dim);
-  if (cache_elem_bytes(cache_dtype) == 0)
-    return fail(AMF_ERR_UNSUPPORTED, "%s: cache dtype %d is not bf16/fp16", who, cache_dtype);
+  const int es = cache_elem_bytes(cache_dtype);
+  if (es == 0)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: cache dtype %d is not bf16/fp16/fp32", who, cache_dtype);
   if (head_dim % 32 != 0)
     return fail(AMF_ERR_UNSUPPORTED, "%s: head_dim %d is not a multiple of 32", who, head_dim);
   int64_t page_elems = (int64_t)block_size * num_heads * head_dim;
-  if (cache_page_stride < page_elems * 2 || !aligned16(cache_page_stride))
+  if (cache_page_stride < page_elems * es || !aligned16(cache_page_stride))
     return fail(AMF_ERR_INVALID_ARG, "%s: cache page stride %lld < page bytes %lld or unaligned",
-                who, (long long)cache_page_stride, (long long)(page_elems * 2));
+                who, (long long)cache_page_stride, (long long)(page_elems * es));
   if (pool_pages <= 0 || pool_pages > 0x7FFFFFFF)
     return fail(AMF_ERR_INVALID_ARG, "%s: bad pool_pages %lld", who, (long long)pool_pages);
   if (n_pages > 0x7FFFFFFF) return fail(AMF_ERR_UNSUPPORTED, "%s: n_pages too large", who);

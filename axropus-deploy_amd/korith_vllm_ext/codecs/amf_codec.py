@@ -152,21 +152,50 @@ class _HipCodec(Codec):
                              f"{tuple(raw_kv.shape)}")
         amf_hip.require_device_tensor(raw_kv, f"{self.FORMAT} compress")
 
+    def _page_tokens(self, T: int) -> int:
+        """Tokens per page for a dense tensor of T tokens along dim -3.
+
+        int4_sym_block blocks 128 tokens (amf_codec.py:353-370): one page of T
+        tokens when T <= 128 (no padding), else 128-token pages.  The
+        per-(page, head) and group formats define 16-token pages.  The
+        per-tensor and per-channel scales do not depend on paging: 16-token
+        pages when 16 divides T, else one page of T tokens up to 256, else
+        zero-padded 16-token pages."""
+        if self.FORMAT == FMT_INT4_BLOCK:
+            return T if 0 < T <= 128 else 128
+        if self.FORMAT in (FMT_FP8_E4M3_PH, FMT_INT4_ASYM_G32):
+            return 16
+        if T % 16 == 0 or T > 256:
+            return 16
+        return max(T, 1)
+
+    def _is_page_tensor(self, x: torch.Tensor) -> bool:
+        """A layer page tensor [2, nb, bs, H, D] whose pages are exactly the
+        dense grouping of [..., T=bs, H, D]: compressed as 2 planes of nb
+        pages instead of 2*nb one-page planes (same codes and scales)."""
+        if x.dim() != 5 or x.shape[0] != 2:
+            return False
+        bs = int(x.shape[2])
+        if self.FORMAT == FMT_INT4_BLOCK:
+            return bs <= 128
+        if self.FORMAT in (FMT_FP8_E4M3_PH, FMT_INT4_ASYM_G32):
+            return bs == 16
+        return True
+
     def compress(self, raw_kv: torch.Tensor) -> CompressedKV:
         self._check_input(raw_kv)
         x = raw_kv.detach().contiguous()
-        if x.dim() == 5 and x.shape[0] == 2:
-            # A layer's page tensor [2, nb, bs, H, D]: K and V planes of nb pages;
-            # the page is the codec's token block (amf_codec.py:368 on this shape).
+        if self._is_page_tensor(x):
             _, nb, bs, H, D = x.shape
             view = _paged.planes_view([x[0], x[1]])
             n_pages, page, T = nb, bs, nb * bs
         else:
             T, H, D = x.shape[-3:]
-            page = _paged.DENSE_PAGE_TOKENS[self.FORMAT]
+            page = self._page_tokens(T)
             view, n_pages, _keep = _paged.dense_view(x, page)
         P = len(view.planes)
         layout = _paged.BlobLayout(self.FORMAT, P, n_pages, page, H, D)
+        layout.validate()
         blob = torch.empty(layout.total_bytes, dtype=torch.uint8, device=raw_kv.device)
         ws = _paged.quant_gather(layout, view, None, [blob.data_ptr()], P)
         absmax = None
@@ -188,14 +217,16 @@ class _HipCodec(Codec):
                             tensor_scale=tensor_scale, shape=shape, dtype_original=dtype,
                             meta=meta)
 
-    def _code_view(self, blob, layout, n_tokens, dtype):
+    def _code_view(self, blob, layout, n_tokens, dtype, shape):
+        """Codes in the input's shape (last dim D, or D/2 packed nibbles): a
+        view of the blob unless token padding forces a copy."""
         P, n, bs, H, D = (layout.n_planes, layout.n_pages, layout.block_size, layout.num_heads,
                           layout.head_dim)
         per_tok = D if layout.family == "fp8" else D // 2
         codes = blob.narrow(0, 0, layout.data_bytes).view(P, n * bs, H, per_tok)
         if dtype is not None:
             codes = codes.view(dtype)
-        return codes[:, :n_tokens]
+        return codes[:, :n_tokens].reshape(*shape[:-1], per_tok)
 
     def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
         raise NotImplementedError
@@ -222,7 +253,7 @@ class FP8E4M3Codec(_HipCodec):
     RATIO = 0.5
 
     def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
-        data = self._code_view(blob, layout, n_tokens, torch.float8_e4m3fn)
+        data = self._code_view(blob, layout, n_tokens, torch.float8_e4m3fn, shape)
         scales = blob.narrow(0, layout.scale_offset, 16).view(torch.float32)
         if absmax is not None:
             scale = tensor_scale_from_absmax(absmax, dtype)
@@ -239,7 +270,7 @@ class FP8PageHeadCodec(_HipCodec):
     RATIO = 0.5
 
     def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
-        data = self._code_view(blob, layout, n_tokens, torch.float8_e4m3fn)
+        data = self._code_view(blob, layout, n_tokens, torch.float8_e4m3fn, shape)
         stride = _paged._align16(layout.plane_param_bytes) // 4
         fl = blob.narrow(0, layout.scale_offset, layout.scale_bytes).view(torch.float32)
         scales = fl.as_strided((layout.n_planes, layout.n_pages, layout.num_heads),
@@ -254,7 +285,7 @@ class INT4PerChannelCodec(_HipCodec):
     RATIO = 0.25
 
     def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
-        data = self._code_view(blob, layout, n_tokens, None)
+        data = self._code_view(blob, layout, n_tokens, None, shape)
         scales = blob.narrow(0, layout.scale_offset, layout.head_dim * 2).view(torch.float16)
         return data, scales, 1.0, {"zero_point": 0}
 
@@ -267,13 +298,18 @@ class INT4PerBlockCodec(_HipCodec):
     RATIO = 0.25
 
     def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
-        data = self._code_view(blob, layout, n_tokens, None)
+        data = self._code_view(blob, layout, n_tokens, None, shape)
         stride = _paged._align16(layout.plane_param_bytes) // 2
         hv = blob.narrow(0, layout.scale_offset, layout.scale_bytes).view(torch.float16)
         scales = hv.as_strided((layout.n_planes, layout.n_pages), (stride, 1))
-        if len(shape) > 3:
-            scales = scales.reshape(*shape[:-3], layout.n_pages)
-        meta = {"block_size": layout.block_size, "n_blocks": layout.n_pages}
+        # [*leading dims, blocks of dim -3] as INT4PerBlockCodec returns them
+        # (amf_codec.py:404); a page tensor has one block per (K/V, page).
+        lead = 1
+        for d in shape[:-3]:
+            lead *= int(d)
+        n_blocks = layout.n_planes * layout.n_pages // lead
+        scales = scales.reshape(*shape[:-3], n_blocks)
+        meta = {"block_size": 128, "n_tokens": int(shape[-3]), "n_blocks": n_blocks}
         return data, scales, 1.0, meta
 
 

@@ -73,6 +73,9 @@ extern "C" {
 
 /* ---- codec formats ------------------------------------------------------
  * Layouts are per plane; n_pages pages of one plane are contiguous.
+ * Cache pages (cache_dtype AMF_DTYPE_BF16, AMF_DTYPE_F16 or AMF_DTYPE_F32)
+ * are [block_size][num_heads][head_dim] row-major; head_dim is a multiple of
+ * 32 (FP8: head_dim/16, INT4 symmetric: head_dim/32 a power of two).
  *
  * AMF_FMT_FP8_E4M3 (reference "fp8_e4m3", amf_codec.py:174-222)
  *   codes  : [n_pages][block_size][num_heads][head_dim] e4m3fn bytes
@@ -160,9 +163,9 @@ int amf_kv_scatter_pages(const uint64_t* in_planes, int64_t in_page_stride,
 /* Save path: gather n_pages pages of each cache plane through block_ids and
  * quantize them into code_planes / param_planes in `format` (an AMF_FMT_FP8_*
  * value).  planes_per_scale (>= 1, dividing n_planes) groups planes for the
- * per-tensor format and is ignored otherwise.  cache_dtype is AMF_DTYPE_BF16 or AMF_DTYPE_F16.  workspace: device
- * fp32 buffer of amf_quant_workspace_bytes() bytes (may be NULL when that is
- * 0); its contents on entry do not matter.
+ * per-tensor format and is ignored otherwise.  workspace: device fp32
+ * buffer of amf_quant_workspace_bytes() bytes (may be NULL when that is 0);
+ * its contents on entry do not matter.
  * Replaces compressed_vram_pool.py:481-508 with FP8E4M3Codec.compress
  * (amf_codec.py:186-209). */
 int amf_fp8_quant_gather(int32_t format,

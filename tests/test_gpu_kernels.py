@@ -91,6 +91,16 @@ def test_raw_out_of_range_id_is_skipped_and_flagged():
 # ------------------------------------------------------------------ codecs --
 
 CODEC_GEOM = dict(L=2, pool=64, n=24, bs=16, H=8, D=128)
+# 48 heads: pages too large for the register-resident save kernels (and, for
+# int4_asym_g32, for the LDS page stage), so the two-read kernels run.
+WIDE_GEOM = dict(L=1, pool=16, n=6, bs=16, H=48, D=128)
+CODEC_CASES = [
+    pytest.param(torch.bfloat16, CODEC_GEOM, id="bf16"),
+    pytest.param(torch.float16, CODEC_GEOM, id="fp16"),
+    pytest.param(torch.float32, CODEC_GEOM, id="fp32"),
+    pytest.param(torch.bfloat16, WIDE_GEOM, id="bf16-48heads"),
+    pytest.param(torch.float32, WIDE_GEOM, id="fp32-48heads"),
+]
 
 
 def _codec_case(dtype, seed, geom=CODEC_GEOM, outliers=True):
@@ -135,10 +145,10 @@ def _seg(blob, off, nbytes):
     return blob[off:off + nbytes]
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_fp8_tensor_format_bitexact(dtype):
-    values, src_ids, dst_ids = _codec_case(dtype, 10)
-    layout, blobs, ws = _save("fp8_e4m3", values, src_ids, dtype)
+@pytest.mark.parametrize("dtype,geom", CODEC_CASES)
+def test_fp8_tensor_format_bitexact(dtype, geom):
+    values, src_ids, dst_ids = _codec_case(dtype, 10, geom)
+    layout, blobs, ws = _save("fp8_e4m3", values, src_ids, dtype, geom)
     want = []
     for l, blob in enumerate(blobs):
         pages = _pages(values, l, src_ids)
@@ -147,16 +157,16 @@ def test_fp8_tensor_format_bitexact(dtype):
         side = _seg(blob, layout.scale_offset, 16).view(torch.float32).cpu()
         assert torch.equal(side, oc.fp8_sidecar(scale))
         want.append(oc.fp8_tensor_decompress(codes, scale, dtype))
-    target = _restore(layout, blobs, dst_ids, dtype)
-    _check_restored(target, dst_ids, want, dtype)
+    target = _restore(layout, blobs, dst_ids, dtype, geom)
+    _check_restored(target, dst_ids, want, dtype, geom)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_fp8_page_head_format_bitexact(dtype):
-    values, src_ids, dst_ids = _codec_case(dtype, 20)
+@pytest.mark.parametrize("dtype,geom", CODEC_CASES)
+def test_fp8_page_head_format_bitexact(dtype, geom):
+    values, src_ids, dst_ids = _codec_case(dtype, 20, geom)
     # one page of layer 0, head 3 all zeros: absmax 0 -> the 1e-8 floor
     values[0, :, int(src_ids[5]), :, 3, :] = 0
-    layout, blobs, _ = _save("fp8_e4m3_ph", values, src_ids, dtype)
+    layout, blobs, _ = _save("fp8_e4m3_ph", values, src_ids, dtype, geom)
     want = []
     for l, blob in enumerate(blobs):
         pages = _pages(values, l, src_ids)
@@ -166,8 +176,8 @@ def test_fp8_page_head_format_bitexact(dtype):
             got = _seg(blob, layout.param_offset(p), layout.plane_param_bytes).view(torch.float32)
             assert torch.equal(got.cpu().view(scales[p].shape), scales[p])
         want.append(oc.fp8_ph_decompress(codes, scales, dtype))
-    target = _restore(layout, blobs, dst_ids, dtype)
-    _check_restored(target, dst_ids, want, dtype)
+    target = _restore(layout, blobs, dst_ids, dtype, geom)
+    _check_restored(target, dst_ids, want, dtype, geom)
 
 
 def test_fp8_encode_every_bf16_in_range():
@@ -214,11 +224,11 @@ def test_fp8_decode_every_code(dtype):
     assert np.array_equal(bits(target[0].cpu()[finite]), bits(want[finite]))
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_int4_sym_block_format_bitexact(dtype):
-    values, src_ids, dst_ids = _codec_case(dtype, 30)
-    values[1, :, int(src_ids[3])] = 0                      # an all-zero page
-    layout, blobs, _ = _save("int4_sym_block", values, src_ids, dtype)
+@pytest.mark.parametrize("dtype,geom", CODEC_CASES)
+def test_int4_sym_block_format_bitexact(dtype, geom):
+    values, src_ids, dst_ids = _codec_case(dtype, 30, geom)
+    values[geom["L"] - 1, :, int(src_ids[3])] = 0          # an all-zero page
+    layout, blobs, _ = _save("int4_sym_block", values, src_ids, dtype, geom)
     want = []
     for l, blob in enumerate(blobs):
         pages = _pages(values, l, src_ids)                 # [2, n, bs, H, D]
@@ -229,14 +239,14 @@ def test_int4_sym_block_format_bitexact(dtype):
             got = _seg(blob, layout.param_offset(p), layout.plane_param_bytes).view(torch.float16)
             assert torch.equal(got.cpu(), scales[p].flatten())
         want.append(oc.int4_block_decompress(packed, scales, tuple(pages.shape), meta, dtype))
-    target = _restore(layout, blobs, dst_ids, dtype)
-    _check_restored(target, dst_ids, want, dtype)
+    target = _restore(layout, blobs, dst_ids, dtype, geom)
+    _check_restored(target, dst_ids, want, dtype, geom)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_int4_sym_channel_format_bitexact(dtype):
-    values, src_ids, dst_ids = _codec_case(dtype, 40)
-    layout, blobs, _ = _save("int4_sym", values, src_ids, dtype)
+@pytest.mark.parametrize("dtype,geom", CODEC_CASES)
+def test_int4_sym_channel_format_bitexact(dtype, geom):
+    values, src_ids, dst_ids = _codec_case(dtype, 40, geom)
+    layout, blobs, _ = _save("int4_sym", values, src_ids, dtype, geom)
     want = []
     for l, blob in enumerate(blobs):
         pages = _pages(values, l, src_ids)
@@ -245,15 +255,15 @@ def test_int4_sym_channel_format_bitexact(dtype):
         got = _seg(blob, layout.scale_offset, layout.shared_param_bytes).view(torch.float16)
         assert torch.equal(got.cpu(), scales)
         want.append(oc.int4_channel_decompress(packed, scales, tuple(pages.shape), dtype))
-    target = _restore(layout, blobs, dst_ids, dtype)
-    _check_restored(target, dst_ids, want, dtype)
+    target = _restore(layout, blobs, dst_ids, dtype, geom)
+    _check_restored(target, dst_ids, want, dtype, geom)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_int4_asym_g32_format_bitexact(dtype):
-    values, src_ids, dst_ids = _codec_case(dtype, 50)
+@pytest.mark.parametrize("dtype,geom", CODEC_CASES)
+def test_int4_asym_g32_format_bitexact(dtype, geom):
+    values, src_ids, dst_ids = _codec_case(dtype, 50, geom)
     values[0, 1, int(src_ids[2]), 4, 5, 32:64] = 1.5       # a constant group
-    layout, blobs, _ = _save("int4_asym_g32", values, src_ids, dtype)
+    layout, blobs, _ = _save("int4_asym_g32", values, src_ids, dtype, geom)
     want = []
     for l, blob in enumerate(blobs):
         pages = _pages(values, l, src_ids)
@@ -265,10 +275,9 @@ def test_int4_asym_g32_format_bitexact(dtype):
             want_p = params[p].flatten().to(torch.int64) & 0xFFFFFFFF
             assert np.array_equal(got_p.cpu().numpy().view(np.uint32).astype(np.int64),
                                   want_p.numpy()), p
-        want.append(oc.int4_asym_decompress(codes, params, 16, CODEC_GEOM["H"], CODEC_GEOM["D"],
-                                            dtype))
-    target = _restore(layout, blobs, dst_ids, dtype)
-    _check_restored(target, dst_ids, want, dtype)
+        want.append(oc.int4_asym_decompress(codes, params, 16, geom["H"], geom["D"], dtype))
+    target = _restore(layout, blobs, dst_ids, dtype, geom)
+    _check_restored(target, dst_ids, want, dtype, geom)
 
 
 # ------------------------------------------------------ decode attention --
