@@ -75,3 +75,24 @@ extern "C" int64_t amf_quant_workspace_bytes(int32_t format, int32_t n_planes,
     default: return 0;
   }
 }
+
+// ---- prefix keys (host) -------------------------------------------------------
+// FNV-1a with the store's offset basis 1469598103934665603 (core/amf_store.cpp:27,
+// amf_kv_manager.py:38) and the 64-bit FNV prime.
+
+namespace {
+constexpr uint64_t kFnvOffset = 1469598103934665603ull;
+constexpr uint64_t kFnvPrime = 1099511628211ull;
+}  // namespace
+
+extern "C" uint64_t amf_fnv1a64(const void* data, int64_t n_bytes, uint64_t h) {
+  const uint8_t* p = static_cast<const uint8_t*>(data);
+  for (int64_t i = 0; i < n_bytes; ++i) h = (h ^ p[i]) * kFnvPrime;
+  return h;
+}
+
+extern "C" uint64_t amf_hash_tokens(const int32_t* tokens, int64_t n_tokens) {
+  uint64_t h = kFnvOffset;
+  for (int64_t i = 0; i < n_tokens; ++i) h = (h ^ (uint64_t)(uint32_t)tokens[i]) * kFnvPrime;
+  return h;
+}

@@ -33,6 +33,9 @@ FMT_FP8_E4M3_PH = "fp8_e4m3_ph"
 FMT_INT4_SYM = "int4_sym"
 FMT_INT4_BLOCK = "int4_sym_block"
 FMT_INT4_ASYM_G32 = "int4_asym_g32"
+# Raw page bytes (no codec): already-quantized 1-byte caches, and the
+# uncompressed snapshot tier.
+FMT_RAW = "raw"
 
 _FMT_IDS = {
     FMT_FP8_E4M3: amf_hip.FMT_FP8_E4M3,
@@ -62,7 +65,9 @@ def _align16(n: int) -> int:
 
 @dataclass(frozen=True)
 class BlobLayout:
-    """Byte layout of one compressed blob (n_pages pages of n_planes planes)."""
+    """Byte layout of one compressed blob (n_pages pages of n_planes planes).
+    elem_bytes is the cache element size of the raw format (codes are then
+    the page bytes themselves)."""
 
     fmt: str
     n_planes: int
@@ -70,6 +75,7 @@ class BlobLayout:
     block_size: int
     num_heads: int
     head_dim: int
+    elem_bytes: int = 1
 
     @property
     def fmt_id(self) -> int:
@@ -77,6 +83,8 @@ class BlobLayout:
 
     @property
     def family(self) -> str:
+        if self.fmt == FMT_RAW:
+            return "raw"
         return "fp8" if self.fmt.startswith("fp8") else "int4"
 
     @property
@@ -85,6 +93,8 @@ class BlobLayout:
 
     @property
     def code_bytes_per_page(self) -> int:
+        if self.family == "raw":
+            return self.page_elems * self.elem_bytes
         return self.page_elems if self.family == "fp8" else self.page_elems // 2
 
     @property
@@ -142,6 +152,10 @@ class BlobLayout:
         return self.scale_offset + plane * _align16(self.plane_param_bytes)
 
     def validate(self) -> None:
+        if self.fmt == FMT_RAW:
+            if self.code_bytes_per_page % 16:
+                raise ValueError("raw pages must be a multiple of 16 bytes")
+            return
         if self.fmt not in _FMT_IDS:
             raise KeyError(f"format {self.fmt!r} has no paged kernel")
         if self.head_dim % 32:
@@ -371,8 +385,14 @@ def quant_gather(layout: BlobLayout, view: CacheView, block_ids, blob_bases: Seq
 
 
 def dequant_scatter(layout: BlobLayout, blob_bases: Sequence[int], planes_per_blob: int,
-                    view: CacheView, block_ids, err_flag: Optional[torch.Tensor] = None) -> None:
+                    view: CacheView, block_ids, err_flag: Optional[torch.Tensor] = None,
+                    n_pages: Optional[int] = None) -> None:
+    """Dequantize the first n_pages pages (default: all) of each plane of the
+    blobs at blob_bases into the cache pages block_ids."""
     layout.validate()
+    n = layout.n_pages if n_pages is None else n_pages
+    if not 0 <= n <= layout.n_pages:
+        raise ValueError(f"n_pages {n} outside [0, {layout.n_pages}]")
     dev = view.device
     n_planes = len(view.planes)
     if n_planes != planes_per_blob * len(blob_bases):
@@ -383,7 +403,7 @@ def dequant_scatter(layout: BlobLayout, blob_bases: Sequence[int], planes_per_bl
     amf_hip.call(
         fn, layout.fmt_id, _ptr(tables.codes), _ptr(tables.params),
         _ptr(amf_hip.address_table(view.planes, dev)), view.page_stride,
-        amf_hip.dtype_tag(view.dtype), _ptr(ids), view.pool_pages, n_planes, layout.n_pages,
+        amf_hip.dtype_tag(view.dtype), _ptr(ids), view.pool_pages, n_planes, n,
         view.block_size, view.num_heads, view.head_dim, _ptr(err_flag), amf_hip.stream_handle(dev),
     )
 

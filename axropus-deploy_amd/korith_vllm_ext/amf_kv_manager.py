@@ -1,0 +1,342 @@
+"""amf_kv_manager.py - AMFK disk snapshots of vLLM's paged KV cache.
+
+API and file format of the reference (korith_vllm_ext/amf_kv_manager.py:
+36-543): a snapshot is `<key>.kv` (56-byte AMFK header, one 32-byte
+(k_off, k_size, v_off, v_size) entry per layer, then the payload K0 V0 K1
+V1 ...) plus `<key>.tok` (the prompt as little-endian int32), named by the
+9-field AMF key.  Files written here and by the reference are byte-identical
+for the same cache contents, including the header's n_kv_heads field, which
+the reference fills from shape[-3] of a gathered [n_blocks, block_size, H, D]
+page stack, i.e. with block_size (amf_kv_manager.py:336-338).
+
+Data movement on the GPU:
+  save    one amf_kv_gather_pages launch gathers the pages of every layer into
+          a device staging buffer laid out as the payload, then one D2H copy
+          into pinned host memory that is written to the file directly;
+  restore the file is read into pinned memory, copied H2D in one transfer,
+          and one amf_kv_scatter_pages launch writes every layer's pages.
+The reference gathers per layer with advanced indexing and copies through
+pageable memory and Python bytes objects (:311-368, 488-523).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import logging
+import os
+import struct
+import time
+from pathlib import Path
+from typing import Any, List, Optional, Sequence
+
+import numpy as np
+import torch
+
+import amf_hip
+
+from . import _paged
+
+logger = logging.getLogger(__name__)
+
+_FNV_OFFSET: int = 1469598103934665603
+_FNV_PRIME: int = 1099511628211
+_U64_MASK: int = (1 << 64) - 1
+
+_AMFK_MAGIC: int = 0x414D464B  # "AMFK"
+_AMFK_VERSION: int = 1
+_HEADER_FMT = "<IIIIIIII QQQ"
+_HEADER_SIZE = struct.calcsize(_HEADER_FMT)
+_LAYER_FMT = "<QQQQ"
+_LAYER_SIZE = struct.calcsize(_LAYER_FMT)
+assert _HEADER_SIZE == 56 and _LAYER_SIZE == 32
+
+# AMF dtype tags (core/amf_direct_kv.h AmfKvDtype).
+_DTYPE_TAG = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}
+
+
+# ------------------------------------------------------------------ keys --
+
+
+def _fnv1a_bytes(data: bytes, h: int = _FNV_OFFSET) -> int:
+    """FNV-1a over bytes from hash h (libamf_hip.so's amf_fnv1a64)."""
+    buf = bytes(data)
+    return int(amf_hip.load().amf_fnv1a64(buf, len(buf), h & _U64_MASK))
+
+
+def amf_hash_tokens(token_ids: Sequence[int]) -> int:
+    """Prefix hash: one FNV-1a step per token on its 32-bit value
+    (reference: amf_kv_manager.py:75-81; amf_hash_tokens of the C ABI)."""
+    arr = np.asarray([int(t) & 0xFFFFFFFF for t in token_ids], dtype=np.uint32)
+    return int(amf_hip.load().amf_hash_tokens(arr.ctypes.data, arr.size))
+
+
+def amf_hash_tenant_id(tenant_id: str) -> int:
+    """FNV-1a over the UTF-8 tenant string; "" hashes to the offset basis."""
+    if not tenant_id:
+        return _FNV_OFFSET
+    return _fnv1a_bytes(tenant_id.encode("utf-8"))
+
+
+def amf_hash_model(model_path: str) -> int:
+    """FNV-1a over a model file's bytes, 0 if it does not exist (reference:
+    amf_kv_manager.py:84-103).  Reads 16 MiB at a time."""
+    path = Path(model_path)
+    if not path.exists():
+        return 0
+    lib = amf_hip.load()
+    h = _FNV_OFFSET
+    buf = bytearray(16 << 20)
+    mv = memoryview(buf)
+    with open(path, "rb") as f:
+        while True:
+            n = f.readinto(mv)
+            if not n:
+                break
+            h = int(lib.amf_fnv1a64((ctypes.c_char * n).from_buffer(buf), n, h))
+    return h
+
+
+def amf_float_bits(v: float) -> int:
+    """IEEE-754 single-precision bit pattern of v."""
+    return struct.unpack("<I", struct.pack("<f", v))[0]
+
+
+def amf_key_filename(model_hash: int, tenant_hash: int, prefix_hash: int, n_ctx: int,
+                     kv_version: int, rope_base_bits: int, rope_scale_bits: int,
+                     sampling_hash: int, rng_hash: int) -> str:
+    """The store's entry base name (AmfStore entry_basename(); reference:
+    amf_kv_manager.py:118-134)."""
+    return (f"amf_{model_hash:016x}_{tenant_hash:016x}_{prefix_hash:016x}"
+            f"_{n_ctx}_{kv_version}_{rope_base_bits}_{rope_scale_bits}"
+            f"_{sampling_hash:016x}_{rng_hash:016x}")
+
+
+# --------------------------------------------------------------- manager --
+
+
+def _kv_planes(layer: torch.Tensor):
+    """(K, V) page arrays of a layer: stacked [2, nb, ...] or one array used
+    for both (reference: amf_kv_manager.py:302-313)."""
+    if layer.dim() == 5 and layer.shape[0] == 2:
+        return layer[0], layer[1]
+    return layer, layer
+
+
+class AmfKvManager:
+    """AMFK snapshot save / restore of vLLM's GPU KV cache.
+
+    cache_engine: any object with `gpu_cache`, a list of per-layer tensors
+    ([2, num_blocks, block_size, H, D] or [num_blocks, block_size, H, D]).
+    Other arguments as the reference (amf_kv_manager.py:155-199)."""
+
+    def __init__(self, cache_engine: Any, amf_store_path: str, model_config: Any, *,
+                 model_hash: int = 0, tenant_id: str = "__shared__", kv_version: int = 1,
+                 rope_base: float = 10000.0, rope_scale: float = 1.0, sampling_hash: int = 0,
+                 rng_hash: int = 0) -> None:
+        self._cache_engine = cache_engine
+        self._store_path = Path(amf_store_path)
+        self._model_config = model_config
+        self._model_hash = model_hash
+        self._tenant_hash = amf_hash_tenant_id(tenant_id)
+        self._kv_version = kv_version
+        self._rope_base_bits = amf_float_bits(rope_base)
+        self._rope_scale_bits = amf_float_bits(rope_scale)
+        self._sampling_hash = sampling_hash
+        self._rng_hash = rng_hash
+        self._store_path.mkdir(parents=True, exist_ok=True)
+        self._hits = 0
+        self._misses = 0
+        self._saves = 0
+        self._restore_ms = 0.0
+
+    # -------------------------------------------------------------- keys --
+
+    def compute_amf_key(self, prompt_tokens: Sequence[int], n_ctx: Optional[int] = None) -> dict:
+        return {
+            "model_hash": self._model_hash,
+            "tenant_hash": self._tenant_hash,
+            "prefix_hash": amf_hash_tokens(prompt_tokens),
+            "n_ctx": n_ctx or getattr(self._model_config, "max_model_len", 0),
+            "kv_version": self._kv_version,
+            "rope_base_bits": self._rope_base_bits,
+            "rope_scale_bits": self._rope_scale_bits,
+            "sampling_hash": self._sampling_hash,
+            "rng_hash": self._rng_hash,
+        }
+
+    def _stem(self, key: dict) -> str:
+        return amf_key_filename(**key)
+
+    def _kv_filename(self, key: dict) -> Path:
+        return self._store_path / (self._stem(key) + ".kv")
+
+    def _tok_filename(self, key: dict) -> Path:
+        return self._store_path / (self._stem(key) + ".tok")
+
+    def has_snapshot(self, prompt_tokens: Sequence[int]) -> bool:
+        return self._kv_filename(self.compute_amf_key(prompt_tokens)).exists()
+
+    # -------------------------------------------------------------- save --
+
+    def save_kv_state(self, prompt_tokens: Sequence[int], block_table: List[int], *,
+                      saved_ms: float = 0.0) -> bool:
+        """Write the snapshot of `block_table`'s pages (every page when the
+        table is empty) of every layer; True on success."""
+        t0 = time.monotonic()
+        key = self.compute_amf_key(prompt_tokens)
+        kv_path = self._kv_filename(key)
+        gpu_cache = self._cache_engine.gpu_cache
+        n_layers = len(gpu_cache)
+        if n_layers == 0:
+            logger.warning("[AMF_VLLM] save: no GPU cache layers")
+            return False
+        view = _paged.cache_view(gpu_cache)
+        amf_hip.require_device_tensor(gpu_cache[0], "AmfKvManager.save_kv_state")
+        n_tokens = len(prompt_tokens)
+        if block_table:
+            _paged.check_block_ids(block_table, view.pool_pages, unique=False)
+            n_blocks, ids = len(block_table), list(block_table)
+        else:
+            n_blocks, ids = view.pool_pages, None
+        page_bytes = view.page_bytes
+        plane_bytes = n_blocks * page_bytes
+        total = 2 * n_layers * plane_bytes
+        k0 = _kv_planes(gpu_cache[0])[0]
+        header = struct.pack(
+            _HEADER_FMT, _AMFK_MAGIC, _AMFK_VERSION, n_layers, n_tokens,
+            int(k0.shape[-3]),  # the reference's shape[-3] of the page stack
+            int(k0.shape[-1]), _DTYPE_TAG.get(view.dtype, 0), 0, total,
+            key["model_hash"], key["prefix_hash"])
+        table = b"".join(struct.pack(_LAYER_FMT, 2 * l * plane_bytes, plane_bytes,
+                                     (2 * l + 1) * plane_bytes, plane_bytes)
+                         for l in range(n_layers))
+        # gather every layer's pages into the payload layout, then one D2H copy
+        staging = torch.empty(total, dtype=torch.uint8, device=view.device)
+        outs = [staging.data_ptr() + i * plane_bytes for i in range(2 * n_layers)]
+        _paged.gather_pages(view, ids, outs, page_bytes, n_blocks)
+        host = torch.empty(total, dtype=torch.uint8, pin_memory=True)
+        host.copy_(staging, non_blocking=True)
+        torch.cuda.current_stream(view.device).synchronize()
+        del staging
+        tmp_path = kv_path.with_suffix(".kv.tmp")
+        try:
+            with open(tmp_path, "wb") as f:
+                f.write(header)
+                f.write(table)
+                f.write(memoryview(host.numpy()))
+            os.replace(tmp_path, kv_path)
+        except OSError as exc:
+            logger.warning("[AMF_VLLM] save: write failed: %s", exc)
+            tmp_path.unlink(missing_ok=True)
+            return False
+        try:
+            toks = np.asarray([int(t) for t in prompt_tokens], dtype="<i4")
+            self._tok_filename(key).write_bytes(toks.tobytes())
+        except OSError as exc:
+            logger.warning("[AMF_VLLM] save: tok write failed: %s", exc)
+        self._saves += 1
+        logger.info("[AMF_VLLM] save: %d layers, %d tokens, %.1f MB in %.0f ms", n_layers,
+                    n_tokens, total / (1 << 20), (time.monotonic() - t0) * 1e3)
+        return True
+
+    # ----------------------------------------------------------- restore --
+
+    def restore_kv_state(self, prompt_tokens: Sequence[int], block_table: List[int]) -> int:
+        """Load the snapshot of prompt_tokens into the pages `block_table` of
+        every layer; the snapshot's token count, or 0 on a miss or an
+        incompatible file (reference: amf_kv_manager.py:406-533)."""
+        t0 = time.monotonic()
+        key = self.compute_amf_key(prompt_tokens)
+        kv_path = self._kv_filename(key)
+        if not kv_path.exists():
+            self._misses += 1
+            return 0
+        try:
+            size = kv_path.stat().st_size
+            if size < _HEADER_SIZE:
+                logger.warning("[AMF_VLLM] restore: blob too small (%d bytes)", size)
+                self._misses += 1
+                return 0
+            blob = torch.empty(size, dtype=torch.uint8, pin_memory=torch.cuda.is_available())
+            with open(kv_path, "rb") as f:
+                f.readinto(memoryview(blob.numpy()))
+        except OSError as exc:
+            logger.warning("[AMF_VLLM] restore: read failed: %s", exc)
+            self._misses += 1
+            return 0
+        raw = memoryview(blob.numpy())
+        (magic, version, n_layers_snap, n_tokens, _heads, _dim, _dtype, _res, _total,
+         _mh, _ph) = struct.unpack_from(_HEADER_FMT, raw, 0)
+        if magic != _AMFK_MAGIC:
+            logger.warning("[AMF_VLLM] restore: wrong magic 0x%08X (expected AMFK)", magic)
+            self._misses += 1
+            return 0
+        if version != _AMFK_VERSION:
+            logger.warning("[AMF_VLLM] restore: version mismatch (got=%d, want=%d)", version,
+                           _AMFK_VERSION)
+            self._misses += 1
+            return 0
+        gpu_cache = self._cache_engine.gpu_cache
+        if n_layers_snap != len(gpu_cache):
+            logger.warning("[AMF_VLLM] restore: layer count mismatch (snap=%d, ctx=%d)",
+                           n_layers_snap, len(gpu_cache))
+            self._misses += 1
+            return 0
+        tbl_end = _HEADER_SIZE + n_layers_snap * _LAYER_SIZE
+        if size < tbl_end:
+            logger.warning("[AMF_VLLM] restore: blob truncated (layer table missing)")
+            self._misses += 1
+            return 0
+        infos = [struct.unpack_from(_LAYER_FMT, raw, _HEADER_SIZE + i * _LAYER_SIZE)
+                 for i in range(n_layers_snap)]
+        if block_table:
+            view = _paged.cache_view(gpu_cache)
+            amf_hip.require_device_tensor(gpu_cache[0], "AmfKvManager.restore_kv_state")
+            _paged.check_block_ids(block_table, view.pool_pages, unique=False)
+            n = len(block_table)
+            want = n * view.page_bytes
+            payload_bytes = size - tbl_end
+            ins: List[int] = []
+            planes: List[int] = []
+            for l, (k_off, k_sz, v_off, v_sz) in enumerate(infos):
+                if k_sz == 0 and v_sz == 0:
+                    continue  # a layer without KV (SSM)
+                for off, sz in ((k_off, k_sz), (v_off, v_sz)):
+                    if sz != want or off + sz > payload_bytes:
+                        raise ValueError(
+                            f"layer {l}: snapshot holds {sz} bytes at {off}, the cache needs "
+                            f"{want} for {n} pages")
+                    ins.append(off)
+                planes += view.planes[2 * l:2 * l + 2]
+            if planes:
+                dev = view.device
+                payload = blob.narrow(0, tbl_end, payload_bytes).to(dev, non_blocking=True)
+                base = payload.data_ptr()
+                sub = _paged.CacheView(planes, view.page_stride, view.pool_pages,
+                                       view.block_size, view.num_heads, view.head_dim, view.dtype,
+                                       dev, keep=view.keep)
+                _paged.scatter_pages([base + o for o in ins], view.page_bytes, sub, block_table, n)
+                torch.cuda.current_stream(dev).synchronize()  # the pinned buffer is reused
+        self._hits += 1
+        self._restore_ms = (time.monotonic() - t0) * 1e3
+        logger.info("[AMF_VLLM] restore: %d layers, %d tokens, %.1f ms", len(gpu_cache),
+                    n_tokens, self._restore_ms)
+        return int(n_tokens)
+
+    def stats(self) -> dict:
+        return {"hits": self._hits, "misses": self._misses, "saves": self._saves,
+                "restore_ms": self._restore_ms}
+
+
+# The name the vLLM integration imports (and the spelling used elsewhere).
+AmfKVManager = AmfKvManager
+
+__all__ = [
+    "AmfKVManager",
+    "AmfKvManager",
+    "amf_float_bits",
+    "amf_hash_model",
+    "amf_hash_tenant_id",
+    "amf_hash_tokens",
+    "amf_key_filename",
+]

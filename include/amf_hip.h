@@ -247,6 +247,18 @@ int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* out, int32_
                                void* workspace, int64_t workspace_bytes,
                                int32_t algo, int32_t* err_flag, void* stream);
 
+/* ---- prefix keys (host functions, no device work) ---------------------------
+ * FNV-1a over bytes, continuing from hash h (pass AMF_FNV_OFFSET to start).
+ * Replaces _fnv1a_bytes (amf_kv_manager.py:69-72; C++ hash_bytes of
+ * core/amf_store.cpp). */
+#define AMF_FNV_OFFSET 1469598103934665603ull
+uint64_t amf_fnv1a64(const void* data, int64_t n_bytes, uint64_t h);
+
+/* Prefix hash of a token sequence: one FNV-1a step per token on its 32-bit
+ * value, h = (h ^ (uint32_t)tok) * prime from AMF_FNV_OFFSET.  Replaces
+ * amf_hash_tokens (amf_kv_manager.py:75-81). */
+uint64_t amf_hash_tokens(const int32_t* tokens, int64_t n_tokens);
+
 /* ---- dense attention ---------------------------------------------------------
  * out = softmax(q k^T * softmax_scale + mask) v, per query row, computed in
  * fp32 and rounded once to out_dtype.  q [batch, num_q_heads, q_len, head_dim],

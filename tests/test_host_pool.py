@@ -1,0 +1,131 @@
+"""Pool allocator, AMFK manager miss paths and keys on the CPU (no device
+work): the slab allocator's first-fit / coalescing / fence bookkeeping, the
+pool refusing a CPU device, AMFK header validation, and the key helpers
+against the oracle's FNV."""
+
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from korith_vllm_ext.amf_kv_manager import (
+    AmfKvManager,
+    AmfKVManager,
+    amf_float_bits,
+    amf_hash_model,
+    amf_hash_tenant_id,
+    amf_hash_tokens,
+    amf_key_filename,
+)
+from korith_vllm_ext.amf_worker_ext import prefix_key
+from korith_vllm_ext.compressed_vram_pool import CompressedVRAMPool, _SlabAllocator
+from oracle import amfk
+
+
+class FakeEvent:
+    def __init__(self, done=False):
+        self.done = done
+
+    def query(self):
+        return self.done
+
+
+def test_allocator_first_fit_and_coalesce():
+    a = _SlabAllocator(10)
+    s1, f1 = a.alloc(3)
+    s2, _ = a.alloc(4)
+    s3, _ = a.alloc(3)
+    assert (s1, s2, s3) == (0, 3, 7) and a.alloc(1) is None and f1 == []
+    a.free(s2, 4, [FakeEvent()])
+    assert a.runs() == [(3, 4)]
+    assert a.alloc(5) is None
+    got = a.alloc(2)
+    assert got[0] == 3 and len(got[1]) == 1          # the span's fence travels with it
+    a.free(0, 3)
+    a.free(7, 3)
+    assert a.runs() == [(0, 3), (5, 5)]
+    a.free(3, 2)
+    assert a.runs() == [(0, 10)] and a.free_blocks() == 10
+    with pytest.raises(ValueError):
+        a.free(2, 2)
+
+
+def test_allocator_prunes_completed_fences():
+    a = _SlabAllocator(8)
+    s, _ = a.alloc(4)
+    t, _ = a.alloc(4)
+    a.free(s, 4, [FakeEvent(done=True)])
+    a.free(t, 4, [FakeEvent(done=False)])
+    start, fences = a.alloc(8)
+    assert start == 0 and len(fences) == 1 and fences[0].done is False
+    a.free(0, 8)
+    a.reset(5)
+    assert a.runs() == [(5, 3)]
+
+
+def test_pool_requires_a_gpu_device():
+    with pytest.raises(RuntimeError):
+        CompressedVRAMPool(num_layers=2, bytes_per_layer=1 << 16, block_bytes=1 << 12,
+                           device="cpu")
+
+
+def test_keys_match_oracle_fnv():
+    toks = list(range(1000)) + [-1, 2**31 - 1]
+    assert amf_hash_tokens(toks) == amfk.hash_tokens(toks)
+    assert amf_hash_tokens([]) == amfk.FNV_OFFSET
+    assert amf_hash_tenant_id("") == amfk.FNV_OFFSET
+    assert amf_hash_tenant_id("nebius") == amfk.hash_tenant("nebius")
+    assert amf_float_bits(1.0) == 0x3F800000
+    assert amf_key_filename(1, 2, 3, 4096, 1, 0, 0, 0, 0) == amfk.key_filename(
+        1, 2, 3, 4096, 1, 0, 0, 0, 0)
+    assert prefix_key("abc") == "abc" and prefix_key(255) == f"{255:016x}"
+    assert prefix_key([1, 2, 3]) == f"{amfk.hash_tokens([1, 2, 3]):016x}"
+    assert AmfKVManager is AmfKvManager
+
+
+def test_hash_model_file(tmp_path):
+    p = tmp_path / "m.bin"
+    data = np.random.default_rng(0).integers(0, 256, 100_000, dtype=np.uint8).tobytes()
+    p.write_bytes(data)
+    assert amf_hash_model(str(p)) == amfk.fnv1a_bytes(data)
+    assert amf_hash_model(str(tmp_path / "missing")) == 0
+
+
+class _Engine:
+    def __init__(self, n_layers):
+        self.gpu_cache = [torch.zeros(2, 4, 16, 2, 64, dtype=torch.bfloat16)
+                          for _ in range(n_layers)]
+
+
+class _Cfg:
+    max_model_len = 4096
+
+
+def _write(mgr, tokens, payload: bytes):
+    mgr._kv_filename(mgr.compute_amf_key(tokens)).write_bytes(payload)
+
+
+def test_manager_restore_miss_paths(tmp_path):
+    mgr = AmfKvManager(_Engine(2), str(tmp_path), _Cfg())
+    toks = [5, 6, 7]
+    assert mgr.restore_kv_state(toks, [0, 1]) == 0                         # no file
+    _write(mgr, toks, b"\x00" * 20)
+    assert mgr.restore_kv_state(toks, [0, 1]) == 0                         # too small
+    hdr = amfk.pack_header(2, 3, 16, 64, 2, 0, 0, 0)
+    _write(mgr, toks, b"XXXX" + hdr[4:])
+    assert mgr.restore_kv_state(toks, [0, 1]) == 0                         # magic
+    _write(mgr, toks, hdr[:4] + struct.pack("<I", 9) + hdr[8:])
+    assert mgr.restore_kv_state(toks, [0, 1]) == 0                         # version
+    _write(mgr, toks, amfk.pack_header(3, 3, 16, 64, 2, 0, 0, 0))
+    assert mgr.restore_kv_state(toks, [0, 1]) == 0                         # layer count
+    _write(mgr, toks, hdr + b"\x00" * 10)
+    assert mgr.restore_kv_state(toks, [0, 1]) == 0                         # table cut
+    assert mgr.stats()["misses"] == 6 and mgr.stats()["hits"] == 0
+    # an empty block table restores nothing but is a hit, as the reference
+    tab = b"".join(struct.pack("<4Q", 0, 0, 0, 0) for _ in range(2))
+    _write(mgr, toks, hdr + tab)
+    assert mgr.restore_kv_state(toks, []) == 3 and mgr.stats()["hits"] == 1
+    assert mgr.has_snapshot(toks) and not mgr.has_snapshot([1])
