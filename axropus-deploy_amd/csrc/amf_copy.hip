@@ -18,7 +18,7 @@ using amf::ld_stream;
 using amf::st_stream;
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = AMF_RESTORE_UNROLL;
 
 __global__ __launch_bounds__(kThreads) void page_copy_kernel(
     const uint64_t* __restrict__ src_planes, int64_t src_stride, const int32_t* __restrict__ src_ids,

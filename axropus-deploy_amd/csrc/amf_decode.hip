@@ -37,6 +37,10 @@
 #include "amf_internal.h"
 #include "amf_kernel_util.h"
 
+// Decode attention is held to a tolerance, not to the codecs' exact
+// operation sequence: let multiplies and adds fuse into FMAs here.
+#pragma clang fp contract(fast)
+
 namespace {
 
 using namespace amf;
@@ -104,22 +108,29 @@ __device__ __forceinline__ float row_sum16(float v) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// 8 nibbles of w (element e in bits 4e..4e+3) -> 8 bf16 values 16 + c as an
-// MFMA operand (element 2i in the low half of dword i).  bf16(16 + c) =
-// 0x4180 | c << 3: the low byte is 0x80 | c << 3, the high byte 0x41.
-__device__ __forceinline__ u32x4 nib8_to_bf16_16c(uint32_t w) {
-  const uint32_t lo = ((w << 3) & 0x78787878u) | 0x80808080u;  // byte i: even nibble 2i
-  const uint32_t hi = ((w >> 1) & 0x78787878u) | 0x80808080u;  // byte i: odd nibble 2i+1
-  const uint32_t z01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // lo0 hi0 lo1 hi1
-  const uint32_t z23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
-  const uint32_t k41 = 0x41414141u;
+// 8 nibbles of w (nibble i in bits 4i..4i+3) -> 8 bf16 values 128 + c as an
+// MFMA operand.  bf16(128 + c) = 0x4300 | c: the code is the low byte and 0x43
+// the high byte, so two masks and four byte permutes build the operand.  The
+// element order is k = [n0 n2 n4 n6 n1 n3 n5 n7] (kNibOfK below); the other
+// operand of the product is laid out in the same order.
+constexpr float kCodeBias = 128.0f;
+
+__device__ __forceinline__ u32x4 nib8_to_bf16_128c(uint32_t w) {
+  const uint32_t ev = w & 0x0F0F0F0Fu;          // bytes: n0 n2 n4 n6
+  const uint32_t od = (w >> 4) & 0x0F0F0F0Fu;   // bytes: n1 n3 n5 n7
+  const uint32_t k43 = 0x43434343u;
   u32x4 r;
-  r[0] = __builtin_amdgcn_perm(k41, z01, 0x04010400u);
-  r[1] = __builtin_amdgcn_perm(k41, z01, 0x04030402u);
-  r[2] = __builtin_amdgcn_perm(k41, z23, 0x04010400u);
-  r[3] = __builtin_amdgcn_perm(k41, z23, 0x04030402u);
+  r[0] = __builtin_amdgcn_perm(k43, ev, 0x04010400u);  // n0, n2
+  r[1] = __builtin_amdgcn_perm(k43, ev, 0x04030402u);  // n4, n6
+  r[2] = __builtin_amdgcn_perm(k43, od, 0x04010400u);  // n1, n3
+  r[3] = __builtin_amdgcn_perm(k43, od, 0x04030402u);  // n5, n7
   return r;
 }
+
+// Nibble index held by operand element k of nib8_to_bf16_128c, and the
+// operand element holding nibble e.
+__host__ __device__ constexpr int nib_of_k(int k) { return k < 4 ? 2 * k : 2 * (k - 4) + 1; }
+__host__ __device__ constexpr int k_of_nib(int e) { return (e & 1) ? 4 + (e >> 1) : (e >> 1); }
 
 __device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -247,6 +258,131 @@ __device__ __forceinline__ int64_t split_page(const SplitPages& sp, int pi, bool
 
 // ============================================================== MFMA path ==
 
+// One 32-token chunk of the MFMA kernel: QK^T, online softmax, PV.  FULL:
+// all 32 tokens are inside the context and both pages are valid.
+#ifndef AMF_DECODE_RESCALE_SLACK
+#define AMF_DECODE_RESCALE_SLACK 8.0f
+#endif
+#ifndef AMF_DECODE_FULL_FAST
+#define AMF_DECODE_FULL_FAST 0
+#endif
+constexpr float kRescaleSlack = AMF_DECODE_RESCALE_SLACK;  // log2 units
+
+template <int R, bool QBF16, bool FULL>
+__device__ __forceinline__ void mfma_chunk(
+    const DecodeArgs& a, const ChunkLoads& cur, const bool (&pok)[2], int c0, int tok_end, int lo,
+    int hi, const u32x4 (&qa_hi)[(R + 3) / 4][4], const u32x4 (&qa_lo)[(R + 3) / 4][4],
+    const float (&qsum)[(R + 3) / 4][4], float (&m_run)[(R + 3) / 4], float (&l_run)[(R + 3) / 4],
+    float (&corr)[(R + 3) / 4], f32x4 (&acc)[(R + 3) / 4][8],
+    float (&p_lds)[(R + 3) / 4][2][4][16]) {
+  constexpr int NT = (R + 3) / 4;
+  const u32x4* kcode = cur.kcode;
+  const u32x4* kpar = cur.kpar;
+  const int vu = hi >> 1, vhalf = hi & 1;
+  const u32x4 vc0 = cur.vc0, vc1 = cur.vc1, vp0 = cur.vp0, vp1 = cur.vp1;
+
+  // ---- QK^T and online softmax ----
+  float x[NT][2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    u32x4 kb[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) kb[st] = nib8_to_bf16_128c(kcode[u][st]);
+    float ks[4], kz[4];
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      ks[gi] = pscale(kpar[u][gi]);
+      kz[gi] = pzero(kpar[u][gi]) - kCodeBias * ks[gi];
+    }
+    const bool valid = FULL || (pok[u] && (c0 + u * kBS + lo) < tok_end);
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      f32x4 cacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        cacc = mfma_bf16(qa_hi[T][st], kb[st], cacc);
+        if constexpr (!QBF16) cacc = mfma_bf16(qa_lo[T][st], kb[st], cacc);
+      }
+      float sc = 0.0f;
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) sc += ks[gi] * cacc[gi] + kz[gi] * qsum[T][gi];
+      x[T][u] = valid ? sc * a.qk_scale_log2 : -__builtin_inff();
+    }
+  }
+
+  float p[NT][2];
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    const float cm = row_max16(fmaxf(x[T][0], x[T][1]));
+    // Lazy rescale: the reference max moves only when a score exceeds it by
+    // more than kRescaleSlack (p stays <= 2^kRescaleSlack), so the
+    // accumulators are rescaled a few times per split, not every chunk.
+    if (__any(cm > m_run[T] + kRescaleSlack)) {
+      const float m_new = fmaxf(m_run[T], cm);
+      const float alpha = exp2_fast(m_run[T] - m_new);
+      l_run[T] *= alpha;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) acc[T][b] *= alpha;
+      // corr lives in the A layout: lane lo holds head 4T + lo/4.
+      corr[T] *= __shfl(alpha, 16 * (lo >> 2));
+      m_run[T] = m_new;
+    }
+    p[T][0] = exp2_fast(x[T][0] - m_run[T]);
+    p[T][1] = exp2_fast(x[T][1] - m_run[T]);
+    l_run[T] += p[T][0] + p[T][1];
+    p_lds[T][0][hi][lo] = p[T][0];
+    p_lds[T][1][hi][lo] = p[T][1];
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  // ---- PV ----
+  u32x4 vb[8];
+  {
+    const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
+#pragma unroll
+    for (int b = 0; b < 8; ++b) vb[b] = nib8_to_bf16_128c(vw[b]);
+  }
+  const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
+  const bool vpage_ok = pok[vu];
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    // A row (r', g) = (4T + lo/4, lo%4), k-slice hi: tokens 8 hi .. 8 hi + 7.
+    const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
+    const float4 pa = pl[0], pb = pl[1];
+    const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+    // Weights w = p * s of the lane's 8 tokens in the operand's k order, as a
+    // bf16 hi + lo pair.  A token outside the context gets a zero param word
+    // (its params may be uninitialised memory), hence w = 0 and no zero-point
+    // term.
+    float wk[8];
+    float cs = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool valid = FULL || (vpage_ok && (c0 + 8 * hi + e) < tok_end);
+      const uint32_t pwe = valid ? pw[e] : 0u;
+      const float sv = pscale(pwe);
+      wk[k_of_nib(e)] = pv[e] * sv;
+      cs += pv[e] * (pzero(pwe) - kCodeBias * sv);
+    }
+    u32x4 ahi, alo;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t hw = pack2<true>(wk[2 * j], wk[2 * j + 1]);
+      ahi[j] = hw;
+      alo[j] = pack2<true>(wk[2 * j] - u2f(hw << 16), wk[2 * j + 1] - u2f(hw & 0xFFFF0000u));
+    }
+    corr[T] += cs;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      acc[T][b] = mfma_bf16(ahi, vb[b], acc[T][b]);
+      acc[T][b] = mfma_bf16(alo, vb[b], acc[T][b]);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+
+
 #ifndef AMF_DECODE_WAVES_PER_EU
 #define AMF_DECODE_WAVES_PER_EU 2
 #endif
@@ -274,20 +410,23 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     // lanes whose k-slice (hi) is group g.
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
+      // Elements in the k order of nib8_to_bf16_128c; an fp16 query is split
+      // into bf16 hi + lo (a bf16 query has lo = 0).
       u32x4 vh = {0, 0, 0, 0}, vl = {0, 0, 0, 0};
       if (r < R && g == hi) {
         const u32x4 raw = *reinterpret_cast<const u32x4*>(qh + r * kD + 32 * hi + 8 * st);
+        float xq[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if constexpr (QBF16) {
-            vh[i] = raw[i];
-          } else {
-            const float x0 = qval<false>((uint16_t)(raw[i] & 0xFFFFu));
-            const float x1 = qval<false>((uint16_t)(raw[i] >> 16));
-            const uint32_t h0 = bf16_bits(x0), h1 = bf16_bits(x1);
-            vh[i] = h0 | (h1 << 16);
-            vl[i] = bf16_bits(x0 - u2f(h0 << 16)) | (bf16_bits(x1 - u2f(h1 << 16)) << 16);
-          }
+          xq[2 * i] = qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu));
+          xq[2 * i + 1] = qval<QBF16>((uint16_t)(raw[i] >> 16));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x0 = xq[nib_of_k(2 * j)], x1 = xq[nib_of_k(2 * j + 1)];
+          const uint32_t hw = pack2<true>(x0, x1);
+          vh[j] = hw;
+          vl[j] = pack2<true>(x0 - u2f(hw << 16), x1 - u2f(hw & 0xFFFF0000u));
         }
       }
       qa_hi[T][st] = vh;
@@ -333,109 +472,19 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
 
   for (int c0 = tok_begin; c0 < tok_end; c0 += 32) {
     const ChunkLoads cur = nxt;
-    bool pok[2] = {pok_n[0], pok_n[1]};
+    const bool pok[2] = {pok_n[0], pok_n[1]};
     const int cn = c0 + 32 <= last_c0 ? c0 + 32 : c0;
     pg_n[0] = split_page(spg, cn / kBS, &pok_n[0]);
     pg_n[1] = split_page(spg, cn / kBS + 1, &pok_n[1]);
     nxt = issue_chunk(a, pg_n[0], pg_n[1], h, lo, hi);
-    const u32x4* kcode = cur.kcode;
-    const u32x4* kpar = cur.kpar;
-    const int vu = hi >> 1, vhalf = hi & 1;
-    const u32x4 vc0 = cur.vc0, vc1 = cur.vc1, vp0 = cur.vp0, vp1 = cur.vp1;
-
-    // ---- QK^T and online softmax ----
-    float x[NT][2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      u32x4 kb[4];
-#pragma unroll
-      for (int st = 0; st < 4; ++st) kb[st] = nib8_to_bf16_16c(kcode[u][st]);
-      float ks[4], kz[4];
-#pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        ks[gi] = pscale(kpar[u][gi]);
-        kz[gi] = pzero(kpar[u][gi]) - 16.0f * ks[gi];
-      }
-      const bool valid = pok[u] && (c0 + u * kBS + lo) < tok_end;
-#pragma unroll
-      for (int T = 0; T < NT; ++T) {
-        f32x4 cacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          cacc = mfma_bf16(qa_hi[T][st], kb[st], cacc);
-          if constexpr (!QBF16) cacc = mfma_bf16(qa_lo[T][st], kb[st], cacc);
-        }
-        float sc = 0.0f;
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) sc += ks[gi] * cacc[gi] + kz[gi] * qsum[T][gi];
-        x[T][u] = valid ? sc * a.qk_scale_log2 : -__builtin_inff();
-      }
-    }
-
-    float p[NT][2];
-#pragma unroll
-    for (int T = 0; T < NT; ++T) {
-      const float cm = row_max16(fmaxf(x[T][0], x[T][1]));
-      const float m_new = fmaxf(m_run[T], cm);
-      if (__any(m_new > m_run[T])) {
-        const float alpha = exp2_fast(m_run[T] - m_new);
-        l_run[T] *= alpha;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) acc[T][b] *= alpha;
-        // corr lives in the A layout: lane lo holds head 4T + lo/4.
-        corr[T] *= __shfl(alpha, 16 * (lo >> 2));
-        m_run[T] = m_new;
-      }
-      p[T][0] = exp2_fast(x[T][0] - m_run[T]);
-      p[T][1] = exp2_fast(x[T][1] - m_run[T]);
-      l_run[T] += p[T][0] + p[T][1];
-      p_lds[T][0][hi][lo] = p[T][0];
-      p_lds[T][1][hi][lo] = p[T][1];
-    }
-    __builtin_amdgcn_wave_barrier();
-
-    // ---- PV ----
-    u32x4 vb[8];
-    {
-      const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
-#pragma unroll
-      for (int b = 0; b < 8; ++b) vb[b] = nib8_to_bf16_16c(vw[b]);
-    }
-    const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
-    const bool vpage_ok = pok[vu];
-#pragma unroll
-    for (int T = 0; T < NT; ++T) {
-      // A row (r', g) = (4T + lo/4, lo%4), k-slice hi: tokens 8 hi .. 8 hi + 7.
-      const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
-      const float4 pa = pl[0], pb = pl[1];
-      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-      u32x4 ahi, alo;
-      float cs = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const bool valid = vpage_ok && (c0 + 8 * hi + e) < tok_end;
-        const float sv = pscale(pw[e]);
-        const float w = valid ? pv[e] * sv : 0.0f;
-        const uint32_t wh = bf16_bits(w);
-        const uint32_t wl = bf16_bits(w - u2f(wh << 16));
-        if (e & 1) {
-          ahi[e >> 1] |= wh << 16;
-          alo[e >> 1] |= wl << 16;
-        } else {
-          ahi[e >> 1] = wh;
-          alo[e >> 1] = wl;
-        }
-        const float zp = pzero(pw[e]) - 16.0f * sv;
-        cs += valid ? pv[e] * zp : 0.0f;
-      }
-      corr[T] += cs;
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        acc[T][b] = mfma_bf16(ahi, vb[b], acc[T][b]);
-        acc[T][b] = mfma_bf16(alo, vb[b], acc[T][b]);
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
+    // A chunk of 32 valid tokens on valid pages (the common case) skips the
+    // per-token masks.
+    if (AMF_DECODE_FULL_FAST && pok[0] && pok[1] && c0 + 32 <= tok_end)
+      mfma_chunk<R, QBF16, true>(a, cur, pok, c0, tok_end, lo, hi, qa_hi, qa_lo, qsum, m_run,
+                                 l_run, corr, acc, p_lds);
+    else
+      mfma_chunk<R, QBF16, false>(a, cur, pok, c0, tok_end, lo, hi, qa_hi, qa_lo, qsum, m_run,
+                                  l_run, corr, acc, p_lds);
   }
 
   // ---- write the split's partial (unnormalised O, m, l) ----
