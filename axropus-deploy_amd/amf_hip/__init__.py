@@ -15,6 +15,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+from collections import OrderedDict
 from typing import Optional, Sequence
 
 ABI_VERSION = 1
@@ -190,11 +191,31 @@ def stream_handle(device) -> int:
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 
+_TABLES: "OrderedDict[tuple, object]" = OrderedDict()
+_TABLES_MAX = 512
+
+
 def address_table(addrs: Sequence[int], device):
-    """Device int64 tensor holding `addrs` (a plane table)."""
+    """Device int64 tensor holding `addrs` (a plane table).
+
+    Tables are immutable and cached by content (least recently used dropped
+    beyond _TABLES_MAX), so a launch over the same cache or blobs as an
+    earlier one costs no host-to-device copy for its tables."""
     import torch
 
-    return torch.tensor(list(addrs), dtype=torch.int64, device=device)
+    dev = torch.device(device)
+    key = (dev.type, dev.index, tuple(int(a) for a in addrs))
+    with _lock:
+        t = _TABLES.get(key)
+        if t is not None:
+            _TABLES.move_to_end(key)
+            return t
+    t = torch.tensor(list(key[2]), dtype=torch.int64, device=dev)
+    with _lock:
+        _TABLES[key] = t
+        while len(_TABLES) > _TABLES_MAX:
+            _TABLES.popitem(last=False)
+    return t
 
 
 def require_device_tensor(t, what: str) -> None:

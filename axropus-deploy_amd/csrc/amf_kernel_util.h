@@ -182,17 +182,19 @@ __device__ __forceinline__ uint32_t f32x4_to_e4m3(const float* x) {
 
 // ---- division ---------------------------------------------------------------
 
-// x / b rounded to nearest even (IEEE).  rb must be the correctly rounded
-// reciprocal RN(1/b).  With AMF_MARKSTEIN_DIV the quotient comes from
+// x / b rounded to nearest even (IEEE) for b > 0.  rb must be the correctly
+// rounded reciprocal RN(1/b).  With AMF_MARKSTEIN_DIV the quotient comes from
 // Markstein's sequence q = RN(x*rb), r = x - b*q (exact via fma),
 // q' = RN(q + r*rb), which returns RN(x/b) for normal operands when rb is
 // RN(1/b) (Markstein 1990; Muller et al., Handbook of Floating-Point
-// Arithmetic, Thm. 4.10); otherwise the compiler's correctly rounded divide.
+// Arithmetic, Thm. 4.10).  The sum q + r*rb turns x = -0 into +0, so the
+// sign of x (the sign of the quotient, b being positive) is put back.
+// Otherwise the compiler's correctly rounded divide.
 __device__ __forceinline__ float div_rn(float x, float b, float rb) {
 #if AMF_MARKSTEIN_DIV
   float q = x * rb;
   float r = __builtin_fmaf(-q, b, x);
-  return __builtin_fmaf(r, rb, q);
+  return __builtin_copysignf(__builtin_fmaf(r, rb, q), x);
 #else
   (void)rb;
   return x / b;

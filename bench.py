@@ -163,6 +163,48 @@ class RestoreCase:
                 "sample": f"restore of {sample_layers} of {self.layers} layers, median of "
                           f"{len(times)} runs ({time.perf_counter() - t_start:.1f} s total)"}
 
+    def save_launch(self):
+        """The save direction on the same shape: gather the prefix pages from
+        the paged cache through the block table and quantize into the blobs."""
+        from korith_vllm_ext import _paged
+
+        return _paged.PreparedCodecLaunch(
+            "save", self.layout, [self.blobs[l].data_ptr() for l in range(self.layers)], 2,
+            _paged.cache_view(self.cache), self.ids)
+
+    def pool_api(self, steps: int, warmup: int) -> dict:
+        """Wall-clock ms per CompressedVRAMPool.put_from_vllm / restore_to_vllm
+        call on this shape (host work included, tables cached after the first
+        call), with the algorithmic GB/s of the same bytes."""
+        from korith_vllm_ext.compressed_vram_pool import CompressedVRAMPool
+
+        blk = 1 << 20
+        per_layer = -(-self.layout.total_bytes // blk) * blk
+        pool = CompressedVRAMPool(self.layers, per_layer, blk, default_format=self.fmt,
+                                  device=DEV)
+        src = seeded_table(self.pool, self.pages, 11).tolist()
+        dst = self.ids.tolist()
+        n_tok = self.pages * 16
+
+        def wall(fn):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / steps
+
+        put_ms = wall(lambda: pool.put_from_vllm("bench", self.cache, src, n_tok))
+        rest_ms = wall(lambda: pool.restore_to_vllm("bench", self.cache, dst))
+        del pool
+        torch.cuda.empty_cache()
+        return {"put_from_vllm_ms": round(put_ms, 4),
+                "put_GB/s": round(self.algo_bytes / put_ms / 1e6, 1),
+                "restore_to_vllm_ms": round(rest_ms, 4),
+                "restore_GB/s": round(self.algo_bytes / rest_ms / 1e6, 1)}
+
     def free(self):
         del self.launch, self.cache, self.blobs
         torch.cuda.empty_cache()
@@ -270,7 +312,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--profile", choices=["fp8_restore", "int4_restore", "decode_mfma",
+    ap.add_argument("--profile", choices=["fp8_restore", "int4_restore", "fp8_save", "int4_save",
+                                          "decode_mfma",
                                           "decode_valu", "copy"], default=None,
                     help="run only this kernel loop (for rocprofv3)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -305,11 +348,12 @@ def main() -> int:
             log(f"copy: {ms:.4f} ms/launch, 1 GiB read + 1 GiB written per launch, "
                 f"{2 * 2**30 / ms / 1e6:.1f} GB/s")
             return 0
-        if args.profile in ("fp8_restore", "int4_restore"):
-            fmt = "fp8_e4m3_ph" if args.profile == "fp8_restore" else "int4_asym_g32"
+        if args.profile in ("fp8_restore", "int4_restore", "fp8_save", "int4_save"):
+            fmt = "fp8_e4m3_ph" if args.profile.startswith("fp8") else "int4_asym_g32"
             case = (RestoreCase(fmt, 32, 8, 128, 8192, 512, 2) if fmt == "fp8_e4m3_ph"
                     else RestoreCase(fmt, 32, 8, 128, 16384, 2048, 3))
-            ms = time_launches(case.launch.launch, args.steps, args.warmup)
+            launch = case.launch if args.profile.endswith("restore") else case.save_launch()
+            ms = time_launches(launch.launch, args.steps, args.warmup)
             log(f"{args.profile}: {ms:.4f} ms/launch, {case.algo_bytes / ms / 1e6:.1f} GB/s")
         else:
             case = DecodeCase()
@@ -354,6 +398,9 @@ def main() -> int:
                                   "sample": cb["sample"], "seconds": round(cb["seconds"], 3),
                                   "cpu": platform.processor() or platform.machine(),
                                   "torch": torch.__version__}
+    log("fp8 restore: CompressedVRAMPool API wall clock")
+    result["pool_api"] = fp8.pool_api(args.steps, args.warmup)
+    log(f"pool api: {result['pool_api']}")
     fp8.free()
     del fp8
 
