@@ -287,6 +287,46 @@ class DecodeCase:
 # -------------------------------------------------------------------- main --
 
 
+def long_context_70b(steps: int, warmup: int) -> dict:
+    """Llama-3-70B share on one GPU: FP8-PH restore of a 131072-token prefix
+    (80 layers x 8192 pages, ~21.5 GB of blobs into a 43 GB bf16 cache) and
+    INT4 decode at batch 8 x 131072 tokens, 64 query heads (GQA 8).  Skipped
+    when the device lacks the ~70 GB it needs."""
+    free, _ = torch.cuda.mem_get_info()
+    if free < 80 * (1 << 30):
+        log(f"70b workloads skipped: {free / 2**30:.0f} GiB free")
+        return {"fp8_restore_70b": None, "decode_70b": None}
+    out = {}
+    log("70b fp8 restore: building inputs")
+    case = RestoreCase("fp8_e4m3_ph", 80, 8, 128, 8192, 8192, 5)
+    ms = time_launches(case.launch.launch, max(3, steps // 4), warmup)
+    gbs = case.algo_bytes / (ms * 1e-3) / 1e9
+    out["fp8_restore_70b"] = {"workload": "fp8_restore_llama3_70b_131k", "ms": round(ms, 4),
+                              "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "algo_bytes": case.algo_bytes}
+    log(f"70b fp8 restore: {ms:.3f} ms, {gbs:.1f} GB/s")
+    case.free()
+    del case
+    log("70b decode: building inputs")
+    dc = DecodeCase(8, 64, 8, 131072, 131072, 6)
+    msd = time_launches(lambda: dc.launch(amf_hip_module().DECODE_MFMA), steps, warmup)
+    gd = dc.algo_bytes / (msd * 1e-3) / 1e9
+    out["decode_70b"] = {"workload": "decode_llama3_70b_b8_131k", "ms_per_layer_call": round(msd, 5),
+                         "tok_per_s_per_layer": round(dc.batch / (msd * 1e-3), 1),
+                         "tok_per_s_model_80_layers": round(dc.batch / (80 * msd * 1e-3), 1),
+                         "GB/s": round(gd, 1), "frac": round(gd / HBM_PEAK_GBS, 4)}
+    log(f"70b decode: {msd:.4f} ms, {gd:.1f} GB/s")
+    del dc
+    torch.cuda.empty_cache()
+    return out
+
+
+def amf_hip_module():
+    import amf_hip
+
+    return amf_hip
+
+
 def profiled_traffic(name: str):
     """HBM bytes per launch recorded by the rocprofv3 FETCH_SIZE / WRITE_SIZE
     runs of this workload (profiles/<name>.md, counters scaled by the
@@ -313,7 +353,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--profile", choices=["fp8_restore", "int4_restore", "fp8_save", "int4_save",
-                                          "decode_mfma",
+                                          "fp8_restore_70b", "decode_70b", "decode_mfma",
                                           "decode_valu", "copy"], default=None,
                     help="run only this kernel loop (for rocprofv3)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -347,6 +387,16 @@ def main() -> int:
             ms = time_launches(fn, args.steps, args.warmup)
             log(f"copy: {ms:.4f} ms/launch, 1 GiB read + 1 GiB written per launch, "
                 f"{2 * 2**30 / ms / 1e6:.1f} GB/s")
+            return 0
+        if args.profile == "fp8_restore_70b":
+            case = RestoreCase("fp8_e4m3_ph", 80, 8, 128, 8192, 8192, 5)
+            ms = time_launches(case.launch.launch, args.steps, args.warmup)
+            log(f"{args.profile}: {ms:.4f} ms/launch, {case.algo_bytes / ms / 1e6:.1f} GB/s")
+            return 0
+        if args.profile == "decode_70b":
+            case = DecodeCase(8, 64, 8, 131072, 131072, 6)
+            ms = time_launches(lambda: case.launch(amf_hip.DECODE_MFMA), args.steps, args.warmup)
+            log(f"{args.profile}: {ms:.4f} ms/call, {case.algo_bytes / ms / 1e6:.1f} GB/s")
             return 0
         if args.profile in ("fp8_restore", "int4_restore", "fp8_save", "int4_save"):
             fmt = "fp8_e4m3_ph" if args.profile.startswith("fp8") else "int4_asym_g32"
@@ -434,6 +484,9 @@ def main() -> int:
             "valu_ms": round(res["valu"], 5), "mfma_over_valu_speedup": round(res["valu"] / msd, 3),
         }
         log(f"int4 decode: mfma {msd:.4f} ms ({gd:.1f} GB/s), valu {res['valu']:.4f} ms")
+        del dc
+        torch.cuda.empty_cache()
+        result.update(long_context_70b(args.steps, args.warmup))
     print(json.dumps(result), flush=True)
     return 0
 

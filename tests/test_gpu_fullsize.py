@@ -67,6 +67,34 @@ def test_restore_fullsize(fmt):
     case.free()
 
 
+def _check_decode(dc, algo, seqs):
+    out = dc.out.float().cpu().numpy()
+    lay = dc.layout
+    cpp = lay.code_bytes_per_page
+    ppp = lay.plane_param_bytes // dc.pool
+    for b in seqs:
+        n = (int(dc.ctx[b]) + 15) // 16
+        pages = dc.bt_cpu[b, :n].long()
+        codes, params = [], []
+        for p in range(2):
+            cb = dc.blob[lay.code_offset(p): lay.code_offset(p) + lay.plane_code_bytes]
+            pb = dc.blob[lay.param_offset(p): lay.param_offset(p) + lay.plane_param_bytes]
+            codes.append(cb.view(dc.pool, cpp)[pages.to(cb.device)].cpu())
+            params.append(pb.view(dc.pool, ppp)[pages.to(pb.device)].cpu().view(torch.int32)
+                          .to(torch.int64) & 0xFFFFFFFF)
+        u, s16, z16 = oc.int4_asym_unlayout(torch.stack(codes), torch.stack(params), 16,
+                                            dc.kv_heads, dc.D)
+        kv32 = oc.int4_asym_dequant_f32(u, s16, z16).numpy()
+        ref = oatt.paged_decode_f64(dc.q[b:b + 1].float().cpu().numpy(), kv32[0], kv32[1],
+                                    np.arange(n)[None], dc.ctx[b:b + 1].numpy())
+        # bf16 output: its own rounding (half an ulp, <= |ref| 2^-8) on top of 2e-2
+        half_ulp = np.abs(ref) * 2.0 ** -8
+        d = np.abs(out[b:b + 1] - ref)
+        assert float((d - (2e-2 + half_ulp)).max()) <= 0.0, (algo, b, float(d.max()))
+        _, mean_rel = attn_errors(out[b:b + 1], ref)
+        assert mean_rel <= 1e-2, (algo, b, mean_rel)
+
+
 def test_decode_fullsize_sampled():
     import amf_hip
 
@@ -74,29 +102,44 @@ def test_decode_fullsize_sampled():
     for algo in (amf_hip.DECODE_MFMA, amf_hip.DECODE_VALU):
         dc.launch(algo)
         torch.cuda.synchronize()
-        out = dc.out.float().cpu().numpy()
-        lay = dc.layout
-        cpp = lay.code_bytes_per_page
-        ppp = lay.plane_param_bytes // dc.pool
-        for b in (0, 7, dc.batch - 1):
-            n = (int(dc.ctx[b]) + 15) // 16
-            pages = dc.bt_cpu[b, :n].long().tolist()
-            codes, params = [], []
-            for p in range(2):
-                cbase, pbase = lay.code_offset(p), lay.param_offset(p)
-                codes.append(torch.stack([dc.blob[cbase + pg * cpp: cbase + (pg + 1) * cpp]
-                                          for pg in pages]).cpu())
-                params.append(torch.stack([dc.blob[pbase + pg * ppp: pbase + (pg + 1) * ppp]
-                                           for pg in pages]).cpu().view(torch.int32)
-                              .to(torch.int64) & 0xFFFFFFFF)
-            u, s16, z16 = oc.int4_asym_unlayout(torch.stack(codes), torch.stack(params), 16,
-                                                dc.kv_heads, dc.D)
-            kv32 = oc.int4_asym_dequant_f32(u, s16, z16).numpy()
-            ref = oatt.paged_decode_f64(dc.q[b:b + 1].float().cpu().numpy(), kv32[0], kv32[1],
-                                        np.arange(n)[None], dc.ctx[b:b + 1].numpy())
-            # bf16 output: its own rounding (half an ulp, <= |ref| 2^-8) on top of 2e-2
-            half_ulp = np.abs(ref) * 2.0 ** -8
-            d = np.abs(out[b:b + 1] - ref)
-            assert float((d - (2e-2 + half_ulp)).max()) <= 0.0, (algo, b, float(d.max()))
-            _, mean_rel = attn_errors(out[b:b + 1], ref)
-            assert mean_rel <= 1e-2, (algo, b, mean_rel)
+        _check_decode(dc, algo, (0, 7, dc.batch - 1))
+
+
+def _free_gib():
+    return torch.cuda.mem_get_info()[0] / 2 ** 30
+
+
+def test_restore_70b_fullsize_sampled():
+    """Llama-3-70B share: FP8-PH restore of a 131072-token prefix (80 layers x
+    8192 pages) into an 8192-page bf16 pool through a random permutation."""
+    if _free_gib() < 75:
+        pytest.skip("needs ~70 GiB of device memory")
+    case = bench.RestoreCase("fp8_e4m3_ph", 80, 8, 128, 8192, 8192, seed=5)
+    sentinel = -3.5
+    for c in case.cache:
+        c.fill_(sentinel)
+    case.launch.launch()
+    torch.cuda.synchronize()
+    for l in range(case.layers):
+        # a permutation of the whole pool: no page keeps the sentinel
+        assert not bool((case.cache[l][:, :, 0, 0, 0] == sentinel).all()), l
+    ids = case.ids.long().to(DEV)
+    for l in (0, 41, 79):
+        want = _oracle_restore(case, l)
+        got = case.cache[l][:, ids].cpu()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"layer {l}"
+    case.free()
+
+
+def test_decode_70b_fullsize_sampled():
+    """Batch 8 x 131072 tokens, 64 query heads over 8 KV heads (GQA 8)."""
+    import amf_hip
+
+    if _free_gib() < 8:
+        pytest.skip("needs device memory")
+    dc = bench.DecodeCase(8, 64, 8, 131072, 131072, 6)
+    dc.launch(amf_hip.DECODE_MFMA)
+    torch.cuda.synchronize()
+    _check_decode(dc, amf_hip.DECODE_MFMA, (0, 7))
+    del dc
+    torch.cuda.empty_cache()
