@@ -755,7 +755,10 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
 #endif
 constexpr int64_t kTargetWaves = AMF_DECODE_TARGET_WAVES;
 constexpr int kMaxSplitTokens = 1024;  // 64 pages: one block-table entry per lane
-constexpr int kMaxSplitsPerSeq = 128;  // bounds the merge's reads of partials
+#ifndef AMF_DECODE_MAX_SPLITS
+#define AMF_DECODE_MAX_SPLITS 128
+#endif
+constexpr int kMaxSplitsPerSeq = AMF_DECODE_MAX_SPLITS;  // bounds the merge's reads of partials
 
 int choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context_len) {
   const int64_t work = (int64_t)num_seqs * num_kv_heads * (max_context_len > 0 ? max_context_len : 1);
