@@ -67,6 +67,16 @@ SIGNATURES = {
         _c_i32,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i32, _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
+    "amf_kv_gather_slots": (
+        _c_i32,
+        [_c_ptr, _c_i64, _c_i32, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i32, _c_i64, _c_i64, _c_ptr,
+         _c_ptr],
+    ),
+    "amf_kv_scatter_slots": (
+        _c_i32,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i32, _c_ptr, _c_i64, _c_i32, _c_i64, _c_i64, _c_ptr,
+         _c_ptr],
+    ),
     "amf_fp8_quant_gather": (
         _c_i32,
         [_c_i32, _c_ptr, _c_i64, _c_i32, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_i64,
@@ -200,19 +210,29 @@ def address_table(addrs: Sequence[int], device):
 
     Tables are immutable and cached by content (least recently used dropped
     beyond _TABLES_MAX), so a launch over the same cache or blobs as an
-    earlier one costs no host-to-device copy for its tables."""
+    earlier one costs no host-to-device copy for its tables.  A table handed
+    out on a stream other than the one it was made on is recorded on that
+    stream, so that dropping it never frees memory a queued kernel still
+    reads."""
     import torch
 
     dev = torch.device(device)
     key = (dev.type, dev.index, tuple(int(a) for a in addrs))
+    cur = torch.cuda.current_stream(dev)
     with _lock:
-        t = _TABLES.get(key)
-        if t is not None:
+        hit = _TABLES.get(key)
+        if hit is not None:
             _TABLES.move_to_end(key)
-            return t
+    if hit is not None:
+        t, streams = hit
+        sid = int(cur.cuda_stream)
+        if sid not in streams:
+            t.record_stream(cur)
+            streams.add(sid)
+        return t
     t = torch.tensor(list(key[2]), dtype=torch.int64, device=dev)
     with _lock:
-        _TABLES[key] = t
+        _TABLES[key] = (t, {int(cur.cuda_stream)})
         while len(_TABLES) > _TABLES_MAX:
             _TABLES.popitem(last=False)
     return t

@@ -459,3 +459,92 @@ class PreparedCodecLaunch:
                            _ptr(self.ids), v.pool_pages, len(v.planes), lay.n_pages,
                            v.block_size, v.num_heads, v.head_dim, _ptr(self.err_flag), s)
         amf_hip.check(self.fn, rc)
+
+
+# ------------------------------------------------------------- token slots --
+
+
+class SlotMap:
+    """A vLLM slot mapping (one slot id per token, slot = block * block_size +
+    offset; reference: AMFReqMeta.make, amf_kv_connector.py:90-115).
+
+    Kept on the host, where the page-structure test runs, and copied once per
+    device for the slot kernels.  A device tensor given here costs one
+    device-to-host copy."""
+
+    def __init__(self, slots) -> None:
+        if isinstance(slots, torch.Tensor):
+            host = slots.detach().reshape(-1).to("cpu", torch.int64)
+        else:
+            host = torch.tensor(list(slots), dtype=torch.int64)
+        self.host = host.contiguous()
+        self.n = int(self.host.numel())
+        self._dev = {}
+
+    @classmethod
+    def of(cls, slots) -> "SlotMap":
+        return slots if isinstance(slots, SlotMap) else cls(slots)
+
+    def on(self, device) -> torch.Tensor:
+        """The slots on `device`, made once; recorded on every other stream
+        that uses them so their memory outlives the kernels queued there."""
+        dev = torch.device(device)
+        key = (dev.type, dev.index)
+        cur = torch.cuda.current_stream(dev)
+        got = self._dev.get(key)
+        if got is None:
+            got = (self.host.to(dev), {int(cur.cuda_stream)})
+            self._dev[key] = got
+        t, streams = got
+        if int(cur.cuda_stream) not in streams:
+            t.record_stream(cur)
+            streams.add(int(cur.cuda_stream))
+        return t
+
+    def check(self, pool_slots: int, n: Optional[int] = None) -> None:
+        """ValueError unless the first n slots lie in [0, pool_slots)."""
+        a = self.host[: self.n if n is None else n]
+        if a.numel() and (int(a.min()) < 0 or int(a.max()) >= pool_slots):
+            raise ValueError(f"slot id out of range [0, {pool_slots}): min {int(a.min())} "
+                             f"max {int(a.max())}")
+
+    def page_ids(self, n_tokens: int, block_size: int) -> Optional[List[int]]:
+        """Block ids when the first n_tokens slots are whole pages in order
+        (token p*block_size + i at slot b_p*block_size + i); None otherwise."""
+        if n_tokens <= 0 or n_tokens > self.n or n_tokens % block_size:
+            return None
+        a = self.host[:n_tokens].view(-1, block_size)
+        first = a[:, 0]
+        if bool((first % block_size != 0).any()):
+            return None
+        if not torch.equal(a, first[:, None] + torch.arange(block_size, dtype=torch.int64)):
+            return None
+        return (first // block_size).tolist()
+
+
+def _row_bytes(view: CacheView) -> int:
+    return view.num_heads * view.head_dim * _elem_size(view.dtype)
+
+
+def gather_slots(view: CacheView, slots: SlotMap, n: int, out_planes: Sequence[int],
+                 out_row_stride: int, err_flag: Optional[torch.Tensor] = None) -> None:
+    """out_planes[i] row j <- the cache row slots[j] of plane i, j < n."""
+    dev = view.device
+    amf_hip.call(
+        "amf_kv_gather_slots", _ptr(amf_hip.address_table(view.planes, dev)), view.page_stride,
+        view.block_size, _ptr(slots.on(dev)), view.pool_pages * view.block_size,
+        _ptr(amf_hip.address_table(out_planes, dev)), out_row_stride, len(view.planes), n,
+        _row_bytes(view), _ptr(err_flag), amf_hip.stream_handle(dev),
+    )
+
+
+def scatter_slots(in_planes: Sequence[int], in_row_stride: int, view: CacheView, slots: SlotMap,
+                  n: int, err_flag: Optional[torch.Tensor] = None) -> None:
+    """The cache row slots[j] of plane i <- in_planes[i] row j, j < n."""
+    dev = view.device
+    amf_hip.call(
+        "amf_kv_scatter_slots", _ptr(amf_hip.address_table(in_planes, dev)), in_row_stride,
+        _ptr(amf_hip.address_table(view.planes, dev)), view.page_stride, view.block_size,
+        _ptr(slots.on(dev)), view.pool_pages * view.block_size, len(view.planes), n,
+        _row_bytes(view), _ptr(err_flag), amf_hip.stream_handle(dev),
+    )

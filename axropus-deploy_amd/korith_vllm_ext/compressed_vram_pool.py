@@ -113,7 +113,8 @@ class PoolEntry:
     # launch bookkeeping (not part of the reference record)
     layout: Optional[_paged.BlobLayout] = None
     cache_dtype: Optional[torch.dtype] = None
-    fence: Optional[torch.cuda.Event] = None
+    # last launch that touched the entry's spans, per stream (stream id -> event)
+    fences: Dict[int, torch.cuda.Event] = field(default_factory=dict)
     pending_absmax: Optional[Tuple[torch.Tensor, torch.cuda.Event]] = None
 
     def nbytes(self) -> int:
@@ -410,13 +411,7 @@ class CompressedVRAMPool:
         L, _, T, H, D = x.shape
         if L > self.num_layers:
             raise ValueError(f"{L} layers exceed the pool's {self.num_layers}")
-        if fmt == FMT_RAW:
-            page = 16 if T % 16 == 0 else T
-        else:
-            if fmt not in POOL_FORMATS:
-                get_codec(fmt)
-                raise KeyError(f"format {fmt!r} has no pool kernel")
-            page = get_codec(fmt)._page_tokens(T)
+        page = self._dense_page(fmt, T)
         n_pages = max(1, -(-T // page))
         Tp = n_pages * page
         x = x.contiguous()
@@ -429,6 +424,15 @@ class CompressedVRAMPool:
         layout = self._layout(fmt, n_pages, page, H, D, x.dtype)
         return self._insert(prefix_hash, fmt, layout, view, None, T, (2, T, H, D), raw_kv.dtype,
                             savings_ms, keep=x)
+
+    def _dense_page(self, fmt: str, T: int) -> int:
+        """Tokens per page of a dense [2, T, H, D] layer entry in `fmt`."""
+        if fmt == FMT_RAW:
+            return 16 if T % 16 == 0 else T
+        if fmt not in POOL_FORMATS:
+            get_codec(fmt)
+            raise KeyError(f"format {fmt!r} has no pool kernel")
+        return get_codec(fmt)._page_tokens(T)
 
     def promote_from_raw(self, prefix_hash: str, raw_kv: torch.Tensor, *,
                          format: Optional[str] = None) -> bool:
@@ -464,6 +468,116 @@ class CompressedVRAMPool:
         flat = out.view(L, 2, lay.n_pages * lay.block_size, lay.num_heads, lay.head_dim)
         res = flat[:, :, :T].reshape(L, *shape)
         return res.to(target_dtype) if res.dtype != target_dtype else res
+
+    # ------------------------------------------------- token-slot paths --
+
+    def put_from_slots(self, prefix_hash: str, gpu_cache: list, slot_mapping, *,
+                       format: Optional[str] = None, savings_ms: float = 0.0) -> bool:
+        """Save the token rows `slot_mapping` (slot = block * block_size +
+        offset) of every layer of vLLM's cache as a dense [L, 2, T, H, D]
+        entry, T = len(slot_mapping): the entry put_from_raw makes from
+        stack([flat(layer)[:, slots] for layer]), which is what the
+        connector's save_kv_layer + wait_for_save store (reference:
+        amf_kv_connector.py:411-422, 446-483).
+
+        Slots that are whole pages in order, with pages as long as the
+        format's dense pages, are quantized straight from the cache pages (one
+        launch for all layers); any other mapping is first gathered into a
+        dense buffer by the slot kernel."""
+        fmt = format or self.default_format
+        if len(gpu_cache) == 0:
+            return False
+        view = _paged.cache_view(gpu_cache)
+        self._check_device(view.device)
+        slots = _paged.SlotMap.of(slot_mapping)
+        T = slots.n
+        if T == 0:
+            return False
+        slots.check(view.pool_pages * view.block_size)
+        if _is_already_compressed(view.dtype):
+            fmt = FMT_RAW
+        L, H, D = view.n_layers, view.num_heads, view.head_dim
+        if L > self.num_layers:
+            raise ValueError(f"{L} layers exceed the pool's {self.num_layers}")
+        page = self._dense_page(fmt, T)
+        ids = slots.page_ids(T, page) if page == view.block_size else None
+        if ids is not None:
+            layout = self._layout(fmt, T // page, page, H, D, view.dtype)
+            return self._insert(prefix_hash, fmt, layout, view, ids, T, (2, T, H, D),
+                                view.dtype, savings_ms)
+        staging = torch.empty(L, 2, T, H, D, dtype=view.dtype, device=view.device)
+        outs = [staging[l, kv].data_ptr() for l in range(L) for kv in range(2)]
+        _paged.gather_slots(view, slots, T, outs, H * D * staging.element_size())
+        return self.put_from_raw(prefix_hash, staging, format=fmt, savings_ms=savings_ms)
+
+    def restore_to_slots(self, prefix_hash: str, gpu_cache: list, slot_mapping, *,
+                         first_layer: int = 0) -> int:
+        """restore_entry_to_slots for the entry under prefix_hash; returns its
+        token count, 0 on a miss."""
+        entry = self.get(prefix_hash)
+        if entry is None:
+            return 0
+        self.restore_entry_to_slots(entry, gpu_cache, slot_mapping, first_layer=first_layer)
+        return entry.num_tokens
+
+    def restore_entry_to_slots(self, entry: PoolEntry, gpu_cache: list, slot_mapping, *,
+                               first_layer: int = 0) -> int:
+        """Write layers first_layer .. first_layer + len(gpu_cache) - 1 of
+        `entry` into the token rows `slot_mapping` of the caches gpu_cache
+        (flat(cache)[:, slots[:n]] = decompress(blob)[:, :n] with n = min(entry
+        tokens, len(slots)); reference: amf_kv_connector.py:345-385).  Returns
+        n, or 0 when the entry has left the pool.
+
+        Page-ordered slots whose pages are as long as the entry's are written
+        by the codec kernel straight into the cache pages; otherwise the
+        layers are decompressed into a dense buffer and moved by the slot
+        kernel (a raw entry is moved by the slot kernel directly)."""
+        with self._lock:
+            if self._index.get(entry.prefix_hash) is not entry:
+                return 0
+            layers = min(len(gpu_cache), entry.num_layers - first_layer)
+            if first_layer < 0 or layers <= 0:
+                return 0
+            view = _paged.cache_view(gpu_cache[:layers])
+            self._check_device(view.device)
+            lay = entry.layout
+            H, D = lay.num_heads, lay.head_dim
+            if (view.num_heads, view.head_dim) != (H, D):
+                raise ValueError(f"cache rows [{view.num_heads}, {view.head_dim}] do not match "
+                                 f"the entry's [{H}, {D}]")
+            if entry.format == FMT_RAW and view.dtype.itemsize != lay.elem_bytes:
+                raise ValueError(f"raw entry of {lay.elem_bytes}-byte elements cannot fill a "
+                                 f"{view.dtype} cache")
+            slots = _paged.SlotMap.of(slot_mapping)
+            T = entry.blobs[0].meta["n_tokens"]
+            n = min(T, slots.n)
+            if n == 0:
+                return 0
+            slots.check(view.pool_pages * view.block_size, n)
+            bases = [self._slabs[b.layer_id].data_ptr() + b.data_offset
+                     for b in entry.blocks[first_layer:first_layer + layers]]
+            P = lay.block_size
+            row = H * D * view.dtype.itemsize
+            self._wait(entry)
+            ids = slots.page_ids(n, P) if P == view.block_size else None
+            if ids is not None and entry.format == FMT_RAW:
+                ins = [base + lay.code_offset(p) for base in bases for p in range(2)]
+                _paged.scatter_pages(ins, lay.code_bytes_per_page, view, ids, n // P)
+            elif ids is not None:
+                _paged.dequant_scatter(lay, bases, 2, view, ids, n_pages=n // P)
+            elif entry.format == FMT_RAW:
+                ins = [base + lay.code_offset(p) for base in bases for p in range(2)]
+                _paged.scatter_slots(ins, row, view, slots, n)
+            else:
+                pages = -(-n // P)
+                staging = torch.empty(2 * layers, pages, P, H, D, dtype=view.dtype,
+                                      device=view.device)
+                planes = [staging[i] for i in range(2 * layers)]
+                _paged.dequant_scatter(lay, bases, 2, _paged.planes_view(planes), None,
+                                       n_pages=pages)
+                _paged.scatter_slots([t.data_ptr() for t in planes], row, view, slots, n)
+            self._fence(entry)
+            return n
 
     def delete(self, prefix_hash: str) -> bool:
         with self._lock:
@@ -578,15 +692,21 @@ class CompressedVRAMPool:
         entry.pending_absmax = None
 
     def _fence(self, entry: PoolEntry) -> None:
+        """Record the current stream's last launch on the entry's spans (one
+        event per stream, so restores queued on several streams all hold the
+        spans until they finish)."""
+        stream = torch.cuda.current_stream(self.device)
         ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.device))
-        entry.fence = ev
+        ev.record(stream)
+        entry.fences[int(stream.cuda_stream)] = ev
 
     def _wait(self, entry: PoolEntry) -> None:
-        """Order this stream after the entry's last launch (its save may have
-        run on another stream)."""
-        if entry.fence is not None:
-            torch.cuda.current_stream(self.device).wait_event(entry.fence)
+        """Order this stream after the entry's launches on other streams (its
+        save may have run elsewhere)."""
+        stream = torch.cuda.current_stream(self.device)
+        for sid, ev in entry.fences.items():
+            if sid != int(stream.cuda_stream):
+                stream.wait_event(ev)
 
     def _allocate(self, L: int, need: int) -> Optional[List[Tuple[int, list]]]:
         """One span of `need` slab blocks on each of the first L layers,
@@ -628,7 +748,7 @@ class CompressedVRAMPool:
 
     def _release_entry(self, entry: PoolEntry) -> None:
         for b in entry.blocks:
-            self._alloc[b.layer_id].free(b.block_id, b.span_blocks, [entry.fence])
+            self._alloc[b.layer_id].free(b.block_id, b.span_blocks, list(entry.fences.values()))
 
     def _allocate_with_compaction(self, L: int, need: int):
         """Allocation with slab compaction as the last resort (reference:
@@ -664,7 +784,7 @@ class CompressedVRAMPool:
             for entry in self._index.values():
                 ev = torch.cuda.Event()
                 ev.record(stream)
-                entry.fence = ev
+                entry.fences = {int(stream.cuda_stream): ev}
 
     def _rewrap(self, entry: PoolEntry, blk: CompressedBlock) -> None:
         old = entry.blobs[blk.layer_id]

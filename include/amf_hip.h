@@ -160,6 +160,31 @@ int amf_kv_scatter_pages(const uint64_t* in_planes, int64_t in_page_stride,
                          int32_t n_planes, int64_t n_pages, int64_t page_bytes,
                          int32_t* err_flag, void* stream);
 
+/* Token-slot gather (the connector's save): out_planes[i] row j <- the cache
+ * row slot_mapping[j] of cache_planes[i], for i < n_planes, j < n_slots.  A
+ * row is one token's H*D elements, row_bytes bytes (a multiple of 16).  Cache
+ * slot s lives at plane + (s / block_size) * cache_page_stride
+ * + (s % block_size) * row_bytes (rows contiguous within a page); dense row j
+ * at out_planes[i] + j * out_row_stride.  slot_mapping: device int64 array of
+ * n_slots slot ids in [0, pool_slots); others are skipped and flagged in
+ * err_flag.
+ * Replaces flat[:, slots, :, :] of korith_vllm_ext/amf_kv_connector.py:411-422. */
+int amf_kv_gather_slots(const uint64_t* cache_planes, int64_t cache_page_stride,
+                        int32_t block_size, const int64_t* slot_mapping, int64_t pool_slots,
+                        const uint64_t* out_planes, int64_t out_row_stride,
+                        int32_t n_planes, int64_t n_slots, int64_t row_bytes,
+                        int32_t* err_flag, void* stream);
+
+/* Token-slot scatter (the connector's load): the cache row slot_mapping[j]
+ * of cache_planes[i] <- in_planes[i] row j.  Addressing as
+ * amf_kv_gather_slots.  Replaces flat_cache[:, slots, ...] = kv_slice of
+ * korith_vllm_ext/amf_kv_connector.py:374-385. */
+int amf_kv_scatter_slots(const uint64_t* in_planes, int64_t in_row_stride,
+                         const uint64_t* cache_planes, int64_t cache_page_stride,
+                         int32_t block_size, const int64_t* slot_mapping, int64_t pool_slots,
+                         int32_t n_planes, int64_t n_slots, int64_t row_bytes,
+                         int32_t* err_flag, void* stream);
+
 /* Save path: gather n_pages pages of each cache plane through block_ids and
  * quantize them into code_planes / param_planes in `format` (an AMF_FMT_FP8_*
  * value).  planes_per_scale (>= 1, dividing n_planes) groups planes for the

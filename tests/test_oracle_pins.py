@@ -19,6 +19,9 @@ Pin map (oracle function -> checks):
   codecs.int4_asym_*            group brute force; constant groups; error bound;
                                 V tile byte formula of include/amf_hip.h
   paging.gather / scatter       loop restatement; scatter(gather) identity
+  paging.*slot*, align, hash    (page, offset) brute force; page-form identity;
+                                hand-worked align values; SHA-256 empty-message
+                                vector
   attention.*                   two independent formulations agree; closed forms
   amfk.*                        FNV goldens (platform/tests/test_vllm_amf.py:
                                 63-122, 350-384); AMFK header
@@ -421,6 +424,55 @@ def test_paging_gather_scatter():
     untouched = np.setdiff1d(np.arange(40), ids2)
     assert np.all(target[:, untouched] == 0xBEEF)
     assert np.array_equal(paging.gather(target, ids2), got)
+
+
+def test_slot_mapping_brute_force_and_quirks():
+    """AMFReqMeta.make's slots (amf_kv_connector.py:90-115) against slots
+    recomputed from (page, offset) pairs, and align_to_block_size's values
+    (:72-74) worked by hand."""
+    assert [paging.align_to_block_size(n, 16) for n in (0, 1, 15, 16, 17, 32, 33)] == \
+        [-16, 0, 0, 0, 16, 16, 32]
+    blocks = [7, 2, 9]
+    slots = paging.slot_mapping(blocks, 4, 10)
+    assert slots == [28, 29, 30, 31, 8, 9, 10, 11, 36, 37]
+    for i, s in enumerate(slots):
+        assert divmod(s, 4) == (blocks[i // 4], i % 4)
+    assert paging.slot_mapping(blocks, 4, -4) == paging.slot_mapping(blocks, 4, 8)
+
+
+def test_slot_gather_scatter_against_pages():
+    """Whole-page slot lists move what the page gather / scatter moves; a
+    single-slot mistake (offset from the wrong page) fails."""
+    rng = np.random.default_rng(1)
+    cache = rng.integers(0, 65536, size=(2, 12, 4, 3, 8), dtype=np.uint16)
+    ids = [5, 0, 11]
+    slots = paging.slot_mapping(ids, 4, 12)
+    rows = paging.gather_slots(cache, slots)
+    assert np.array_equal(rows.reshape(2, 3, 4, 3, 8), paging.gather(cache, ids))
+    target = np.zeros_like(cache)
+    paging.scatter_slots(target, slots, rows)
+    assert np.array_equal(paging.gather(target, ids), paging.gather(cache, ids))
+    assert np.all(np.delete(target, ids, axis=1) == 0)
+    # unordered slots: every row lands where its slot says
+    perm = rng.permutation(48)[:17]
+    got = paging.gather_slots(cache, perm)
+    for j, s in enumerate(perm):
+        assert np.array_equal(got[:, j], cache[:, s // 4, s % 4])
+    wrong = [(s // 4) * 4 + (s + 1) % 4 for s in slots]
+    assert not np.array_equal(paging.gather_slots(cache, wrong), rows)
+
+
+def test_prefix_hash_known_answers():
+    """The SHA-256 digest of the empty message (published test vector), and
+    the word packing: token 0x00636261 is the bytes b"abc\\x00", -1 is four
+    0xff bytes, and tokens are taken mod 2**32."""
+    assert paging.prefix_hash([]) == "e3b0c44298fc1c14"
+    import hashlib
+
+    assert paging.prefix_hash([0x00636261]) == hashlib.sha256(b"abc\x00").hexdigest()[:16]
+    assert paging.prefix_hash([-1]) == hashlib.sha256(b"\xff" * 4).hexdigest()[:16]
+    assert paging.prefix_hash([1 << 32 | 5]) == paging.prefix_hash([5])
+    assert paging.prefix_hash([1, 2]) != paging.prefix_hash([2, 1])
 
 
 # ------------------------------------------------------------- attention ----
