@@ -194,15 +194,38 @@ def dtype_tag(dtype) -> int:
     raise ValueError(f"unsupported dtype {dtype}")
 
 
-def stream_handle(device) -> int:
-    """hipStream_t of torch's current stream on `device` (0 = null stream)."""
+def _device_index(device) -> int:
     import torch
 
-    return int(torch.cuda.current_stream(device).cuda_stream)
+    if not torch.cuda.is_initialized():
+        torch.cuda.init()
+    if isinstance(device, int):
+        return device
+    dev = torch.device(device)
+    return torch.cuda.current_device() if dev.index is None else dev.index
+
+
+def stream_handle(device) -> int:
+    """hipStream_t of torch's current stream on `device` (0 = null stream);
+    torch's raw-stream query, without building a Stream object."""
+    import torch
+
+    return int(torch._C._cuda_getCurrentRawStream(_device_index(device)))
 
 
 _TABLES: "OrderedDict[tuple, object]" = OrderedDict()
 _TABLES_MAX = 512
+
+
+def to_device(host, device):
+    """Copy a host tensor to `device` through pinned memory, queued on the
+    current stream (no host wait for the stream's earlier work)."""
+    import torch
+
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        return host.to(dev)
+    return host.pin_memory().to(dev, non_blocking=True)
 
 
 def address_table(addrs: Sequence[int], device):
@@ -218,21 +241,20 @@ def address_table(addrs: Sequence[int], device):
 
     dev = torch.device(device)
     key = (dev.type, dev.index, tuple(int(a) for a in addrs))
-    cur = torch.cuda.current_stream(dev)
+    sid = stream_handle(dev)
     with _lock:
         hit = _TABLES.get(key)
         if hit is not None:
             _TABLES.move_to_end(key)
     if hit is not None:
         t, streams = hit
-        sid = int(cur.cuda_stream)
         if sid not in streams:
-            t.record_stream(cur)
+            t.record_stream(torch.cuda.current_stream(dev))
             streams.add(sid)
         return t
-    t = torch.tensor(list(key[2]), dtype=torch.int64, device=dev)
+    t = to_device(torch.tensor(list(key[2]), dtype=torch.int64), dev)
     with _lock:
-        _TABLES[key] = (t, {int(cur.cuda_stream)})
+        _TABLES[key] = (t, {sid})
         while len(_TABLES) > _TABLES_MAX:
             _TABLES.popitem(last=False)
     return t

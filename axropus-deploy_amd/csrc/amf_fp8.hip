@@ -115,32 +115,58 @@ __global__ __launch_bounds__(kThreads) void fp8_dequant_scatter_kernel(
 
 // ------------------------------------------------------------------- save --
 
-// Per-tensor absmax (first of the three per-tensor save kernels): a
-// workgroup's page max goes to its scale group's slot ws[plane / pps] by an
-// integer atomic max on the non-negative float's bit pattern.
+// Per-tensor absmax (first of the three per-tensor save kernels): each
+// workgroup folds a strided set of one plane's pages, then sends its max to
+// the scale group's slot ws[plane / pps] by one integer atomic max on the
+// non-negative float's bit pattern.  All groups' slots share a cache line, so
+// the workgroup count (kAbsBlocks over all planes) bounds the atomics that
+// line serializes.  A page's rows are contiguous: it is read as a flat run of
+// 16-byte vectors, kAbsUnroll of them in flight per lane before any is
+// reduced.
+constexpr int kAbsUnroll = 8;
+constexpr int kAbsBlocks = 2048;
+
+template <int DT>
+__device__ __forceinline__ float absmax16(const u32x4& v, float m) {
+  if constexpr (DT == AMF_DTYPE_F32) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) m = fmaxf(m, fabsf(u2f(v[q])));
+  } else {
+    float x[8];
+    unpack8<DT == AMF_DTYPE_BF16>(v, x);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[q]));
+  }
+  return m;
+}
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void fp8_absmax_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
-    const int32_t* __restrict__ block_ids, int64_t pool, PageGeom g, uint32_t* ws,
-    int32_t* err_flag) {
-  const int64_t j = blockIdx.x;
+    const int32_t* __restrict__ block_ids, int64_t pool, int64_t n_pages, PageGeom g,
+    uint32_t* ws, int32_t* err_flag) {
   const int plane = blockIdx.y;
-  const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
-  if (sp < 0 || sp >= pool) {
-    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
-    return;
-  }
-  const uint8_t* __restrict__ src =
-      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
-  const int col = lane_col(g), rpi = rows_per_iter(g);
+  const int n16 = g.n_rows * g.head_dim * elem_bytes<DT>() / 16;
   float m = 0.0f;
-  for (int r = lane_row0(g); r < g.n_rows; r += rpi) {
-    const uint8_t* p = src + elem_bytes<DT>() * ((int64_t)r * g.head_dim + col * 16);
-    float x[16];
-    load8<DT>(p, x);
-    load8<DT>(p + 8 * elem_bytes<DT>(), x + 8);
+  for (int64_t j = blockIdx.x; j < n_pages; j += gridDim.x) {
+    const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
+    if (sp < 0 || sp >= pool) {
+      if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+      continue;
+    }
+    const u32x4* __restrict__ src = reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride);
+    for (int base = threadIdx.x; base < n16; base += kThreads * kAbsUnroll) {
+      u32x4 v[kAbsUnroll];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(x[q]));
+      for (int u = 0; u < kAbsUnroll; ++u) {
+        const int k = base + u * kThreads;
+        if (k < n16) v[u] = src[k];
+      }
+#pragma unroll
+      for (int u = 0; u < kAbsUnroll; ++u)
+        if (base + u * kThreads < n16) m = absmax16<DT>(v[u], m);
+    }
   }
   m = wave_max_xor(m, 64);
   __shared__ uint32_t s_max;
@@ -430,9 +456,13 @@ extern "C" int amf_fp8_quant_gather(int32_t format, const uint64_t* cache_planes
   const int n_groups = n_planes / g.pps;
   if (pt) {
     fill_u32_kernel<<<(n_groups + 255) / 256, 256, 0, s>>>(ws, n_groups, 0u);
+    const int64_t per_plane = std::max<int64_t>(
+        1, std::min<int64_t>(n_pages, (kAbsBlocks + n_planes - 1) / n_planes));
+    dim3 agrid((unsigned)per_plane, (unsigned)n_planes);
     AMF_WITH_DTYPE(cache_dtype,
-                   fp8_absmax_kernel<DT><<<grid, kThreads, 0, s>>>(
-                       cache_planes, cache_page_stride, block_ids, pool_pages, g, ws, err_flag));
+                   fp8_absmax_kernel<DT><<<agrid, kThreads, 0, s>>>(
+                       cache_planes, cache_page_stride, block_ids, pool_pages, n_pages, g, ws,
+                       err_flag));
   }
   if (looped) {
 #define AMF_LAUNCH(T)                                                                         \

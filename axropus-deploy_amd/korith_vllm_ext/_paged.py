@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
+from functools import cached_property
 from typing import List, Optional, Sequence, Tuple
 
 import torch
@@ -77,39 +78,39 @@ class BlobLayout:
     head_dim: int
     elem_bytes: int = 1
 
-    @property
+    @cached_property
     def fmt_id(self) -> int:
         return _FMT_IDS[self.fmt]
 
-    @property
+    @cached_property
     def family(self) -> str:
         if self.fmt == FMT_RAW:
             return "raw"
         return "fp8" if self.fmt.startswith("fp8") else "int4"
 
-    @property
+    @cached_property
     def page_elems(self) -> int:
         return self.block_size * self.num_heads * self.head_dim
 
-    @property
+    @cached_property
     def code_bytes_per_page(self) -> int:
         if self.family == "raw":
             return self.page_elems * self.elem_bytes
         return self.page_elems if self.family == "fp8" else self.page_elems // 2
 
-    @property
+    @cached_property
     def plane_code_bytes(self) -> int:
         return self.n_pages * self.code_bytes_per_page
 
-    @property
+    @cached_property
     def data_bytes(self) -> int:
         return self.n_planes * self.plane_code_bytes
 
-    @property
+    @cached_property
     def shared_params(self) -> bool:
         return self.fmt in (FMT_FP8_E4M3, FMT_INT4_SYM)
 
-    @property
+    @cached_property
     def plane_param_bytes(self) -> int:
         """Param bytes of one plane (0 for the shared-param formats)."""
         n, H, D = self.n_pages, self.num_heads, self.head_dim
@@ -121,7 +122,7 @@ class BlobLayout:
             return n * H * self.block_size * (D // 32) * 4
         return 0
 
-    @property
+    @cached_property
     def shared_param_bytes(self) -> int:
         if self.fmt == FMT_FP8_E4M3:
             return 16  # [k_scale, v_scale, q_scale, prob_scale] fp32
@@ -129,17 +130,17 @@ class BlobLayout:
             return self.head_dim * 2
         return 0
 
-    @property
+    @cached_property
     def scale_offset(self) -> int:
         return _align16(self.data_bytes)
 
-    @property
+    @cached_property
     def scale_bytes(self) -> int:
         if self.shared_params:
             return self.shared_param_bytes
         return (self.n_planes - 1) * _align16(self.plane_param_bytes) + self.plane_param_bytes
 
-    @property
+    @cached_property
     def total_bytes(self) -> int:
         return self.scale_offset + self.scale_bytes
 
@@ -282,13 +283,17 @@ def dense_view(x: torch.Tensor, page_tokens: int) -> Tuple[CacheView, int, torch
 
 
 def _device_ids(ids, device) -> Optional[torch.Tensor]:
+    """Block ids as a device int32 tensor; host ids travel through pinned
+    memory, queued on the current stream without a host wait."""
     if ids is None:
         return None
+    if isinstance(ids, torch.Tensor) and ids.device.type != "cpu":
+        return ids.to(device=device, dtype=torch.int32).contiguous()
     if isinstance(ids, torch.Tensor):
-        t = ids.to(device=device, dtype=torch.int32)
+        host = ids.to(torch.int32).contiguous()
     else:
-        t = torch.tensor(list(ids), dtype=torch.int32, device=device)
-    return t.contiguous()
+        host = torch.tensor(list(ids), dtype=torch.int32)
+    return amf_hip.to_device(host, device)
 
 
 def check_block_ids(ids: Sequence[int], pool_pages: int, *, unique: bool) -> None:
@@ -480,6 +485,8 @@ class SlotMap:
         self.host = host.contiguous()
         self.n = int(self.host.numel())
         self._dev = {}
+        self._checked = set()
+        self._pages = {}
 
     @classmethod
     def of(cls, slots) -> "SlotMap":
@@ -490,27 +497,40 @@ class SlotMap:
         that uses them so their memory outlives the kernels queued there."""
         dev = torch.device(device)
         key = (dev.type, dev.index)
-        cur = torch.cuda.current_stream(dev)
+        return self._cached_on(key, dev, lambda: amf_hip.to_device(self.host, dev))
+
+    def _cached_on(self, key, dev, make) -> torch.Tensor:
+        sid = amf_hip.stream_handle(dev)
         got = self._dev.get(key)
         if got is None:
-            got = (self.host.to(dev), {int(cur.cuda_stream)})
+            got = (make(), {sid})
             self._dev[key] = got
         t, streams = got
-        if int(cur.cuda_stream) not in streams:
-            t.record_stream(cur)
-            streams.add(int(cur.cuda_stream))
+        if sid not in streams:
+            t.record_stream(torch.cuda.current_stream(dev))
+            streams.add(sid)
         return t
 
     def check(self, pool_slots: int, n: Optional[int] = None) -> None:
         """ValueError unless the first n slots lie in [0, pool_slots)."""
-        a = self.host[: self.n if n is None else n]
+        n = self.n if n is None else n
+        if (pool_slots, n) in self._checked:
+            return
+        a = self.host[:n]
         if a.numel() and (int(a.min()) < 0 or int(a.max()) >= pool_slots):
             raise ValueError(f"slot id out of range [0, {pool_slots}): min {int(a.min())} "
                              f"max {int(a.max())}")
+        self._checked.add((pool_slots, n))
 
     def page_ids(self, n_tokens: int, block_size: int) -> Optional[List[int]]:
         """Block ids when the first n_tokens slots are whole pages in order
         (token p*block_size + i at slot b_p*block_size + i); None otherwise."""
+        key = (n_tokens, block_size)
+        if key not in self._pages:
+            self._pages[key] = self._page_ids(n_tokens, block_size)
+        return self._pages[key]
+
+    def _page_ids(self, n_tokens: int, block_size: int) -> Optional[List[int]]:
         if n_tokens <= 0 or n_tokens > self.n or n_tokens % block_size:
             return None
         a = self.host[:n_tokens].view(-1, block_size)
@@ -520,6 +540,16 @@ class SlotMap:
         if not torch.equal(a, first[:, None] + torch.arange(block_size, dtype=torch.int64)):
             return None
         return (first // block_size).tolist()
+
+    def page_ids_on(self, n_tokens: int, block_size: int, device) -> Optional[torch.Tensor]:
+        """page_ids as a device int32 tensor, made once per device."""
+        ids = self.page_ids(n_tokens, block_size)
+        if ids is None:
+            return None
+        dev = torch.device(device)
+        return self._cached_on((dev.type, dev.index, n_tokens, block_size), dev,
+                               lambda: amf_hip.to_device(torch.tensor(ids, dtype=torch.int32),
+                                                         dev))
 
 
 def _row_bytes(view: CacheView) -> int:

@@ -24,11 +24,11 @@ put_from_raw on save):
   which quantizes the request's pages of every layer in one launch (or
   gathers unordered slots with the slot kernel first).  The entry is the
   one the reference's stack + put_from_raw makes.
-* load: start_load_kv queues, layer by layer, the restore of every hit
-  request into its slots on a load stream and records one event per layer;
-  wait_for_layer_load(layer) makes the forward's stream wait for that
-  layer's event only, so layer l's attention runs while layers > l are still
-  being restored.  extra_config "load_stream": "current" queues the loads
+* load: start_load_kv queues the restore of every hit request into its
+  slots on a load stream, in launches of 1, 1, 2, 4, 8, ... consecutive
+  layers, each followed by an event; wait_for_layer_load(layer) makes the
+  forward's stream wait for its launch's event only, so layer l's attention
+  runs while later layers are still being restored.  extra_config "load_stream": "current" queues the loads
   on the forward's own stream instead (the reference's ordering).
 
 The scheduler-side logic (prefix hash, block alignment, metadata) follows
@@ -52,7 +52,10 @@ import logging
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Any, Dict, List, Optional, Tuple
 
+import numpy as np
 import torch
+
+import amf_hip
 
 from ._paged import SlotMap
 
@@ -120,13 +123,20 @@ logger = logging.getLogger("amf_kv_connector")
 # ------------------------------------------------------------------ helpers --
 
 
+def _token_words(token_ids) -> bytes:
+    """The tokens mod 2**32 as consecutive 4-byte little-endian words."""
+    try:
+        a = np.asarray(token_ids, dtype=np.int64)
+    except (OverflowError, TypeError, ValueError):
+        return b"".join(int(t & 0xFFFFFFFF).to_bytes(4, "little") for t in token_ids)
+    return (a & 0xFFFFFFFF).astype("<u4").tobytes()
+
+
 def _prefix_hash(token_ids) -> str:
     """First 16 hex digits of SHA-256 over the tokens as 4-byte little-endian
-    words (reference: amf_kv_connector.py:64-69)."""
-    h = hashlib.sha256()
-    for t in token_ids:
-        h.update(int(t & 0xFFFFFFFF).to_bytes(4, "little"))
-    return h.hexdigest()[:16]
+    words (reference: amf_kv_connector.py:64-69, which feeds the words one
+    update at a time; the digest of the concatenation is the same)."""
+    return hashlib.sha256(_token_words(token_ids)).hexdigest()[:16]
 
 
 def align_to_block_size(num_tokens: int, block_size: int) -> int:
@@ -147,6 +157,26 @@ def _layer_index(layer_name: str) -> Optional[int]:
             except ValueError:
                 pass
     return None
+
+
+def _layer_groups(layers: List[Tuple[int, str, torch.Tensor]]) -> List[list]:
+    """Split index-sorted (index, name, cache) layers into launch groups of
+    1, 1, 2, 4, 8, ... consecutive layers of one geometry: the first layers
+    are ready after a short launch, the later ones, needed later, come in
+    larger launches with less host work per layer."""
+    groups: List[list] = []
+    cap = 1
+    for item in layers:
+        g = groups[-1] if groups else None
+        if (g is not None and len(g) < cap and item[0] == g[-1][0] + 1
+                and item[2].shape == g[-1][2].shape and item[2].stride() == g[-1][2].stride()
+                and item[2].dtype == g[-1][2].dtype):
+            g.append(item)
+            continue
+        if g is not None:
+            cap = len(groups[-1]) * 2 if len(groups) > 1 else 1
+        groups.append([item])
+    return groups
 
 
 # ----------------------------------------------------------------- metadata --
@@ -170,12 +200,12 @@ class AMFReqMeta:
         """Slots of the first align_to_block_size(len(token_ids)) tokens:
         block b_i's slots b_i * block_size + [0, block_size) in block order."""
         valid = align_to_block_size(len(token_ids), block_size)
-        blocks = torch.tensor(block_ids, dtype=torch.int64).reshape(-1, 1)
+        blocks = torch.from_numpy(np.asarray(block_ids, dtype=np.int64)).reshape(-1, 1)
         slots = (blocks * block_size + torch.arange(block_size, dtype=torch.int64)).flatten()
         return AMFReqMeta(
             request_id=request_id,
             prefix_hash=prefix_hash,
-            token_ids=torch.tensor(token_ids[:valid]),
+            token_ids=torch.from_numpy(np.asarray(token_ids[:valid], dtype=np.int64)),
             slot_mapping=slots[:valid],
             is_store=is_store,
             num_tokens=valid,
@@ -217,10 +247,12 @@ class AMFKVConnector(KVConnectorBase_V1):
 
         # prefix hash -> layer name -> (cache tensor of that layer, request slots)
         self._save_layers: Dict[str, Dict[str, Tuple[torch.Tensor, SlotMap]]] = {}
+        self._save_slots: Dict[str, SlotMap] = {}  # request id -> its slots, this step
         self._known_hashes: set = set()
         self._layer_idx_cache: Dict[str, Optional[int]] = {}
         self._load_stream: Optional[torch.cuda.Stream] = None
         self._layer_events: Dict[str, torch.cuda.Event] = {}
+        self._waited: set = set()  # (event, stream) pairs already waited this step
 
         logger.info(
             "[AMF_CONNECTOR] init role=%s layers=%d heads=%d head_dim=%d bytes_per_layer=%d "
@@ -342,12 +374,14 @@ class AMFKVConnector(KVConnectorBase_V1):
         return None
 
     def start_load_kv(self, forward_context: Any, **kwargs: Any) -> None:
-        """Restore every hit request of this step into its slots, layer by
-        layer, on the load stream (reference: :326-392, which restores
-        request by request on the forward's stream before returning)."""
+        """Restore every hit request of this step into its slots, in layer
+        groups, on the load stream (reference: :326-392, which restores
+        request by request and layer by layer on the forward's stream before
+        returning)."""
         metadata = self._get_connector_metadata()
         assert isinstance(metadata, AMFConnectorMetadata)
         self._layer_events.clear()
+        self._waited.clear()
         pool = self._ensure_pool()
         if pool is None or getattr(forward_context, "attn_metadata", None) is None:
             return
@@ -389,20 +423,26 @@ class AMFKVConnector(KVConnectorBase_V1):
                 self._load_stream = torch.cuda.Stream(device)  # default priority
             stream = self._load_stream
             stream.wait_stream(forward)
+        paged = []
+        for idx, name, kv in layers:
+            pk = self._paged_layer(kv)
+            if pk is None:
+                logger.warning("[AMF_CONNECTOR] Unexpected kv_cache shape %s for %s",
+                               tuple(kv.shape), name)
+                continue
+            paged.append((idx, name, pk))
         with torch.cuda.stream(stream):
-            for idx, name, kv in layers:
-                paged = self._paged_layer(kv)
-                if paged is None:
-                    logger.warning("[AMF_CONNECTOR] Unexpected kv_cache shape %s for %s",
-                                   tuple(kv.shape), name)
-                    continue
+            for group in _layer_groups(paged):
+                first = group[0][0]
+                caches = [pk for _, _, pk in group]
                 for req, entry, slots in hits:
-                    if idx < entry.num_layers:
-                        pool.restore_entry_to_slots(entry, [paged], slots, first_layer=idx)
+                    if first < entry.num_layers:
+                        pool.restore_entry_to_slots(entry, caches, slots, first_layer=first)
                 if self._side_load:
                     ev = torch.cuda.Event()
                     ev.record(stream)
-                    self._layer_events[name] = ev
+                    for _, name, _ in group:
+                        self._layer_events[name] = ev
         for req, _, _ in hits:
             logger.info("[AMF_CONNECTOR] Loaded prefix=%s into paged buffer",
                         req.prefix_hash[:12])
@@ -411,7 +451,11 @@ class AMFKVConnector(KVConnectorBase_V1):
         """Order the forward's stream after the restore of `layer_name` (no
         host wait)."""
         ev = self._layer_events.pop(layer_name, None)
-        if ev is not None:
+        if ev is None:
+            return
+        key = (id(ev), amf_hip.stream_handle(self._pool.device))
+        if key not in self._waited:  # layers of one launch share its event
+            self._waited.add(key)
             torch.cuda.current_stream(self._pool.device).wait_event(ev)
 
     def save_kv_layer(self, layer_name: str, kv_layer: torch.Tensor, attn_metadata: Any,
@@ -431,8 +475,10 @@ class AMFKVConnector(KVConnectorBase_V1):
                     logger.warning("[AMF_CONNECTOR] Unexpected kv_layer shape %s for %s",
                                    tuple(kv_layer.shape), layer_name)
                     return
-            n = min(int(req.slot_mapping.shape[0]), req.num_tokens)
-            slots = SlotMap(req.slot_mapping[:n])
+            slots = self._save_slots.get(req.request_id)
+            if slots is None:
+                n = min(int(req.slot_mapping.shape[0]), req.num_tokens)
+                slots = self._save_slots[req.request_id] = SlotMap(req.slot_mapping[:n])
             self._save_layers.setdefault(req.prefix_hash, {})[layer_name] = (paged, slots)
 
     def wait_for_save(self) -> None:
@@ -443,6 +489,7 @@ class AMFKVConnector(KVConnectorBase_V1):
             # every restore of the step is ordered before the next step's work,
             # also for a layer whose wait_for_layer_load never came
             torch.cuda.current_stream(pool.device).wait_stream(self._load_stream)
+        self._save_slots.clear()
         if pool is None or not self._save_layers:
             self._save_layers.clear()
             return

@@ -205,13 +205,15 @@ class _HipCodec(Codec):
 
     def wrap_blob(self, storage: torch.Tensor, offset: int, layout: "_paged.BlobLayout",
                   shape: tuple, dtype: torch.dtype, absmax: Optional[float],
-                  n_tokens: int) -> CompressedKV:
+                  n_tokens: int, scale: Optional[float] = None) -> CompressedKV:
         """CompressedKV whose tensors are views of storage[offset:] (a blob of
         `layout`).  absmax: the scale group's absmax after a per-tensor FP8
-        save (gives the reference's Python-double tensor_scale)."""
+        save (gives the reference's Python-double tensor_scale); scale: that
+        tensor_scale when the caller already has it or will set it later (no
+        device read either way)."""
         blob = storage.narrow(0, offset, layout.total_bytes)
         data, scales, tensor_scale, meta = self._views(blob, layout, shape, dtype, absmax,
-                                                       n_tokens)
+                                                       n_tokens, scale)
         meta.update({"_blob": blob, "_layout": layout, "n_tokens": n_tokens})
         return CompressedKV(format=self.FORMAT, data=data, scales=scales,
                             tensor_scale=tensor_scale, shape=shape, dtype_original=dtype,
@@ -228,7 +230,7 @@ class _HipCodec(Codec):
             codes = codes.view(dtype)
         return codes[:, :n_tokens].reshape(*shape[:-1], per_tok)
 
-    def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
+    def _views(self, blob, layout, shape, dtype, absmax, n_tokens, scale=None):
         raise NotImplementedError
 
     def decompress_to(self, compressed: CompressedKV,
@@ -252,10 +254,12 @@ class FP8E4M3Codec(_HipCodec):
     FORMAT = FMT_FP8_E4M3
     RATIO = 0.5
 
-    def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
+    def _views(self, blob, layout, shape, dtype, absmax, n_tokens, scale=None):
         data = self._code_view(blob, layout, n_tokens, torch.float8_e4m3fn, shape)
         scales = blob.narrow(0, layout.scale_offset, 16).view(torch.float32)
-        if absmax is not None:
+        if scale is not None:
+            pass
+        elif absmax is not None:
             scale = tensor_scale_from_absmax(absmax, dtype)
         else:
             scale = float(scales[0])
@@ -269,7 +273,7 @@ class FP8PageHeadCodec(_HipCodec):
     FORMAT = FMT_FP8_E4M3_PH
     RATIO = 0.5
 
-    def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
+    def _views(self, blob, layout, shape, dtype, absmax, n_tokens, scale=None):
         data = self._code_view(blob, layout, n_tokens, torch.float8_e4m3fn, shape)
         stride = _paged._align16(layout.plane_param_bytes) // 4
         fl = blob.narrow(0, layout.scale_offset, layout.scale_bytes).view(torch.float32)
@@ -284,7 +288,7 @@ class INT4PerChannelCodec(_HipCodec):
     FORMAT = FMT_INT4_SYM
     RATIO = 0.25
 
-    def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
+    def _views(self, blob, layout, shape, dtype, absmax, n_tokens, scale=None):
         data = self._code_view(blob, layout, n_tokens, None, shape)
         scales = blob.narrow(0, layout.scale_offset, layout.head_dim * 2).view(torch.float16)
         return data, scales, 1.0, {"zero_point": 0}
@@ -297,7 +301,7 @@ class INT4PerBlockCodec(_HipCodec):
     BLOCK = 128
     RATIO = 0.25
 
-    def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
+    def _views(self, blob, layout, shape, dtype, absmax, n_tokens, scale=None):
         data = self._code_view(blob, layout, n_tokens, None, shape)
         stride = _paged._align16(layout.plane_param_bytes) // 2
         hv = blob.narrow(0, layout.scale_offset, layout.scale_bytes).view(torch.float16)
@@ -320,7 +324,7 @@ class INT4AsymG32Codec(_HipCodec):
     FORMAT = FMT_INT4_ASYM_G32
     RATIO = 0.3125  # (0.5 code bytes + 4 param bytes / 32) per element, over 2 bytes
 
-    def _views(self, blob, layout, shape, dtype, absmax, n_tokens):
+    def _views(self, blob, layout, shape, dtype, absmax, n_tokens, scale=None):
         P, n = layout.n_planes, layout.n_pages
         data = blob.narrow(0, 0, layout.data_bytes).view(P, n, layout.code_bytes_per_page)
         stride = _paged._align16(layout.plane_param_bytes) // 4

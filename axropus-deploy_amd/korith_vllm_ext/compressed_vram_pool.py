@@ -500,7 +500,7 @@ class CompressedVRAMPool:
         if L > self.num_layers:
             raise ValueError(f"{L} layers exceed the pool's {self.num_layers}")
         page = self._dense_page(fmt, T)
-        ids = slots.page_ids(T, page) if page == view.block_size else None
+        ids = slots.page_ids_on(T, page, view.device) if page == view.block_size else None
         if ids is not None:
             layout = self._layout(fmt, T // page, page, H, D, view.dtype)
             return self._insert(prefix_hash, fmt, layout, view, ids, T, (2, T, H, D),
@@ -559,7 +559,7 @@ class CompressedVRAMPool:
             P = lay.block_size
             row = H * D * view.dtype.itemsize
             self._wait(entry)
-            ids = slots.page_ids(n, P) if P == view.block_size else None
+            ids = slots.page_ids_on(n, P, view.device) if P == view.block_size else None
             if ids is not None and entry.format == FMT_RAW:
                 ins = [base + lay.code_offset(p) for base in bases for p in range(2)]
                 _paged.scatter_pages(ins, lay.code_bytes_per_page, view, ids, n // P)
@@ -657,7 +657,9 @@ class CompressedVRAMPool:
                                         tensor_scale=1.0, shape=shape, dtype_original=dtype,
                                         meta={"_layout": layout, "n_tokens": T})
                 else:
-                    blob = codec.wrap_blob(self._slabs[l], off, layout, shape, dtype, None, T)
+                    # per-tensor FP8: the scale arrives with pending_absmax
+                    blob = codec.wrap_blob(self._slabs[l], off, layout, shape, dtype, None, T,
+                                           scale=0.0 if pending is not None else None)
                 blobs.append(blob)
                 blocks.append(CompressedBlock(
                     layer_id=l, block_id=start, format=fmt, num_tokens=n_tokens,
@@ -703,9 +705,11 @@ class CompressedVRAMPool:
     def _wait(self, entry: PoolEntry) -> None:
         """Order this stream after the entry's launches on other streams (its
         save may have run elsewhere)."""
-        stream = torch.cuda.current_stream(self.device)
-        for sid, ev in entry.fences.items():
-            if sid != int(stream.cuda_stream):
+        sid = amf_hip.stream_handle(self.device)
+        others = [ev for s, ev in entry.fences.items() if s != sid]
+        if others:
+            stream = torch.cuda.current_stream(self.device)
+            for ev in others:
                 stream.wait_event(ev)
 
     def _allocate(self, L: int, need: int) -> Optional[List[Tuple[int, list]]]:
@@ -794,7 +798,8 @@ class CompressedVRAMPool:
             return
         codec = get_codec(entry.format)
         new = codec.wrap_blob(self._slabs[blk.layer_id], blk.data_offset, entry.layout, old.shape,
-                              entry.cache_dtype, None, old.meta["n_tokens"])
+                              entry.cache_dtype, None, old.meta["n_tokens"],
+                              scale=old.tensor_scale)
         new.tensor_scale = old.tensor_scale
         if "sidecar" in old.meta:
             new.meta["sidecar"] = old.meta["sidecar"]

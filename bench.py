@@ -210,6 +210,151 @@ class RestoreCase:
         torch.cuda.empty_cache()
 
 
+# --------------------------------------------------------------- connector --
+
+
+class ConnectorCase:
+    """AMFKVConnector on the Llama-3-8B shape: a cold prefill of `tokens`
+    prompt tokens saved from 32 layers of a paged bf16 cache, then a warm
+    request restored into other pages through start_load_kv and the
+    per-layer waits.  Also times the raw token-slot kernels on unordered
+    slots (the general path)."""
+
+    def __init__(self, fmt: str = "fp8_e4m3", layers: int = 32, heads: int = 8,
+                 head_dim: int = 128, pool: int = 8192, pages: int = 512, seed: int = 12):
+        from types import SimpleNamespace as NS
+
+        from korith_vllm_ext.amf_kv_connector import AMFKVConnector, KVConnectorRole
+
+        self.layers, self.heads, self.head_dim, self.pages = layers, heads, head_dim, pages
+        self.fmt = fmt
+        self.cache = [device_kv((2, pool, 16, heads, head_dim), head_dim, seed * 100 + l)
+                      for l in range(layers)]
+        self.target = [torch.empty_like(c) for c in self.cache]
+        tokens = pages * 16 + 1
+        self.prompt = list(range(tokens))
+        self.cold = seeded_table(pool, pages + 1, seed).tolist()
+        self.warm = seeded_table(pool, pages + 1, seed + 1).tolist()
+        from korith_vllm_ext import _paged
+
+        page = _paged.DENSE_PAGE_TOKENS[fmt]
+        blob = _paged.BlobLayout(fmt, 2, -(-pages * 16 // page), page, heads, head_dim)
+        extra = dict(num_layers=layers, num_kv_heads=heads, head_dim=head_dim,
+                     bytes_per_layer=(-(-blob.total_bytes // (1 << 20)) + 1) << 20,
+                     default_format=fmt, min_prefix_tokens=64)
+        cfg = NS(cache_config=NS(block_size=16),
+                 kv_transfer_config=NS(kv_connector_extra_config=extra))
+        self.conn = AMFKVConnector(cfg, KVConnectorRole.WORKER)
+        self.NS = NS
+
+    def _sched(self, req_id, blocks):
+        NS = self.NS
+        return NS(scheduled_new_reqs=[NS(req_id=req_id, prompt_token_ids=self.prompt,
+                                         block_ids=(blocks,))],
+                  scheduled_cached_reqs=NS(req_ids=[], resumed_req_ids=set(),
+                                           num_computed_tokens=[], new_block_ids=[]),
+                  num_scheduled_tokens={})
+
+    def _forward(self, caches):
+        NS = self.NS
+        return NS(attn_metadata=object(), virtual_engine=0, no_compile_layers={
+            f"model.layers.{l}.self_attn.attn": NS(kv_cache=[c]) for l, c in enumerate(caches)})
+
+    def save_meta(self):
+        """Scheduler side of a cold request: hash, slots, store metadata."""
+        return self.conn.build_connector_meta(self._sched("cold", self.cold))
+
+    def load_meta(self):
+        """Scheduler side of a warm request: hit, slots, load metadata."""
+        c = self.conn
+        c.update_state_after_alloc(self.NS(request_id="warm"), None, self.pages * 16)
+        return c.build_connector_meta(self._sched("warm", self.warm))
+
+    def save(self, meta):
+        """Worker side of a cold prefill: every layer's save_kv_layer, then
+        wait_for_save (the pool insert)."""
+        c = self.conn
+        c.bind_connector_metadata(meta)
+        fwd = self._forward(self.cache)
+        for name, layer in fwd.no_compile_layers.items():
+            c.save_kv_layer(name, layer.kv_cache[0], None)
+        c.wait_for_save()
+        c.clear_connector_metadata()
+
+    def load(self, meta):
+        """Worker side of a warm request: start_load_kv and every layer's
+        wait_for_layer_load."""
+        c = self.conn
+        c.bind_connector_metadata(meta)
+        fwd = self._forward(self.target)
+        c.start_load_kv(fwd)
+        for name in fwd.no_compile_layers:
+            c.wait_for_layer_load(name)
+        c.wait_for_save()
+        c.clear_connector_metadata()
+
+    @property
+    def tokens(self) -> int:
+        return self.pages * 16
+
+    def algo_bytes(self) -> int:
+        """Codes + params read (restore) or written (save), plus the bf16 rows
+        written (restore) or read (save)."""
+        from korith_vllm_ext import _paged
+
+        lay = _paged.BlobLayout(self.fmt, 2, self.pages, 16, self.heads, self.head_dim)
+        return self.layers * (lay.data_bytes + lay.scale_bytes +
+                              2 * self.tokens * self.heads * self.head_dim * 2)
+
+    def slot_launch(self, seed: int = 5):
+        """Raw token-slot gather of `tokens` unordered slots of every plane."""
+        from korith_vllm_ext import _paged
+
+        S = self.cache[0].shape[1] * 16
+        slots = torch.randperm(S, generator=torch.Generator().manual_seed(seed))[:self.tokens]
+        sm = _paged.SlotMap(slots)
+        view = _paged.cache_view(self.cache)
+        out = torch.empty(self.layers * 2, self.tokens, self.heads, self.head_dim,
+                          dtype=torch.bfloat16, device=DEV)
+        outs = [out[i].data_ptr() for i in range(out.shape[0])]
+        row = self.heads * self.head_dim * 2
+        bytes_moved = 2 * out.numel() * 2
+        return (lambda: _paged.gather_slots(view, sm, self.tokens, outs, row)), bytes_moved, out
+
+    def run(self, steps: int, warmup: int) -> dict:
+        def wall(fn):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / steps
+
+        meta_ms = wall(self.save_meta)
+        smeta = self.save_meta()
+        save_ms = wall(lambda: self.save(smeta))
+        lmeta = self.load_meta()
+        load_ms = wall(lambda: self.load(lmeta))
+        algo = self.algo_bytes()
+        fn, moved, keep = self.slot_launch()
+        slot_ms = time_launches(fn, steps, warmup)
+        del keep
+        return {"workload": "connector_llama3_8b_8k", "format": self.fmt,
+                "tokens": self.tokens, "layers": self.layers,
+                "scheduler_meta_ms": round(meta_ms, 4),
+                "save_ms": round(save_ms, 4), "save_GB/s": round(algo / save_ms / 1e6, 1),
+                "load_ms": round(load_ms, 4), "load_GB/s": round(algo / load_ms / 1e6, 1),
+                "slot_gather_unordered_ms": round(slot_ms, 4),
+                "slot_gather_GB/s": round(moved / slot_ms / 1e6, 1),
+                "slot_gather_frac": round(moved / slot_ms / 1e6 / HBM_PEAK_GBS, 4)}
+
+    def free(self):
+        del self.conn, self.cache, self.target
+        torch.cuda.empty_cache()
+
+
 # ------------------------------------------------------------------ decode --
 
 
@@ -354,7 +499,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--profile", choices=["fp8_restore", "int4_restore", "fp8_save", "int4_save",
                                           "fp8_restore_70b", "decode_70b", "decode_mfma",
-                                          "decode_valu", "copy"], default=None,
+                                          "decode_valu", "copy", "slot_copy"], default=None,
                     help="run only this kernel loop (for rocprofv3)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
@@ -387,6 +532,12 @@ def main() -> int:
             ms = time_launches(fn, args.steps, args.warmup)
             log(f"copy: {ms:.4f} ms/launch, 1 GiB read + 1 GiB written per launch, "
                 f"{2 * 2**30 / ms / 1e6:.1f} GB/s")
+            return 0
+        if args.profile == "slot_copy":
+            cc = ConnectorCase()
+            fn, moved, keep = cc.slot_launch()
+            ms = time_launches(fn, args.steps, args.warmup)
+            log(f"slot_copy: {ms:.4f} ms/launch, {moved / ms / 1e6:.1f} GB/s")
             return 0
         if args.profile == "fp8_restore_70b":
             case = RestoreCase("fp8_e4m3_ph", 80, 8, 128, 8192, 8192, 5)
@@ -486,6 +637,12 @@ def main() -> int:
         log(f"int4 decode: mfma {msd:.4f} ms ({gd:.1f} GB/s), valu {res['valu']:.4f} ms")
         del dc
         torch.cuda.empty_cache()
+        log("connector: save / load through AMFKVConnector")
+        cc = ConnectorCase()
+        result["connector"] = cc.run(args.steps, args.warmup)
+        log(f"connector: {result['connector']}")
+        cc.free()
+        del cc
         result.update(long_context_70b(args.steps, args.warmup))
     print(json.dumps(result), flush=True)
     return 0

@@ -30,6 +30,8 @@ def test_prefix_hash_and_align_match_oracle():
     for n in (0, 1, 7, 64, 300):
         toks = rng.integers(-(1 << 33), 1 << 33, size=n).tolist()
         assert _prefix_hash(toks) == paging.prefix_hash(toks)
+    big = [1 << 70, -(1 << 65) - 3, 7]                 # beyond int64: the word-by-word route
+    assert _prefix_hash(big) == paging.prefix_hash(big)
     for n in range(-3, 70):
         for bs in (1, 4, 16):
             assert align_to_block_size(n, bs) == paging.align_to_block_size(n, bs)
