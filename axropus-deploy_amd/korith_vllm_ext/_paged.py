@@ -556,6 +556,23 @@ def _row_bytes(view: CacheView) -> int:
     return view.num_heads * view.head_dim * _elem_size(view.dtype)
 
 
+def token_pages(view: CacheView, page_tokens: int) -> Optional[CacheView]:
+    """The same planes cut in pages of page_tokens rows: the view itself when
+    its pages already hold page_tokens rows, else a re-cut when the token
+    rows are evenly spaced (pages unpadded), page p then starting at token
+    row p * page_tokens.  None otherwise."""
+    if page_tokens == view.block_size:
+        return view
+    row = _row_bytes(view)
+    if view.page_stride != view.block_size * row:
+        return None
+    n = view.pool_pages * view.block_size // page_tokens
+    if n == 0:
+        return None
+    return CacheView(view.planes, page_tokens * row, n, page_tokens, view.num_heads,
+                     view.head_dim, view.dtype, view.device, keep=view.keep)
+
+
 def gather_slots(view: CacheView, slots: SlotMap, n: int, out_planes: Sequence[int],
                  out_row_stride: int, err_flag: Optional[torch.Tensor] = None) -> None:
     """out_planes[i] row j <- the cache row slots[j] of plane i, j < n."""

@@ -480,8 +480,9 @@ class CompressedVRAMPool:
         connector's save_kv_layer + wait_for_save store (reference:
         amf_kv_connector.py:411-422, 446-483).
 
-        Slots that are whole pages in order, with pages as long as the
-        format's dense pages, are quantized straight from the cache pages (one
+        Slots that come in aligned runs as long as the format's dense pages
+        (whole vLLM blocks of that length, or of any multiple of it when the
+        cache's pages are unpadded) are quantized straight from the cache (one
         launch for all layers); any other mapping is first gathered into a
         dense buffer by the slot kernel."""
         fmt = format or self.default_format
@@ -500,10 +501,11 @@ class CompressedVRAMPool:
         if L > self.num_layers:
             raise ValueError(f"{L} layers exceed the pool's {self.num_layers}")
         page = self._dense_page(fmt, T)
-        ids = slots.page_ids_on(T, page, view.device) if page == view.block_size else None
+        pview = _paged.token_pages(view, page)
+        ids = slots.page_ids_on(T, page, view.device) if pview is not None else None
         if ids is not None:
             layout = self._layout(fmt, T // page, page, H, D, view.dtype)
-            return self._insert(prefix_hash, fmt, layout, view, ids, T, (2, T, H, D),
+            return self._insert(prefix_hash, fmt, layout, pview, ids, T, (2, T, H, D),
                                 view.dtype, savings_ms)
         staging = torch.empty(L, 2, T, H, D, dtype=view.dtype, device=view.device)
         outs = [staging[l, kv].data_ptr() for l in range(L) for kv in range(2)]
@@ -528,10 +530,10 @@ class CompressedVRAMPool:
         tokens, len(slots)); reference: amf_kv_connector.py:345-385).  Returns
         n, or 0 when the entry has left the pool.
 
-        Page-ordered slots whose pages are as long as the entry's are written
-        by the codec kernel straight into the cache pages; otherwise the
-        layers are decompressed into a dense buffer and moved by the slot
-        kernel (a raw entry is moved by the slot kernel directly)."""
+        Slots in aligned runs as long as the entry's pages are written by the
+        codec kernel straight into the cache; otherwise the layers are
+        decompressed into a dense buffer and moved by the slot kernel (a raw
+        entry is moved by the slot kernel directly)."""
         with self._lock:
             if self._index.get(entry.prefix_hash) is not entry:
                 return 0
@@ -559,12 +561,13 @@ class CompressedVRAMPool:
             P = lay.block_size
             row = H * D * view.dtype.itemsize
             self._wait(entry)
-            ids = slots.page_ids_on(n, P, view.device) if P == view.block_size else None
+            pview = _paged.token_pages(view, P)
+            ids = slots.page_ids_on(n, P, view.device) if pview is not None else None
             if ids is not None and entry.format == FMT_RAW:
                 ins = [base + lay.code_offset(p) for base in bases for p in range(2)]
-                _paged.scatter_pages(ins, lay.code_bytes_per_page, view, ids, n // P)
+                _paged.scatter_pages(ins, lay.code_bytes_per_page, pview, ids, n // P)
             elif ids is not None:
-                _paged.dequant_scatter(lay, bases, 2, view, ids, n_pages=n // P)
+                _paged.dequant_scatter(lay, bases, 2, pview, ids, n_pages=n // P)
             elif entry.format == FMT_RAW:
                 ins = [base + lay.code_offset(p) for base in bases for p in range(2)]
                 _paged.scatter_slots(ins, row, view, slots, n)

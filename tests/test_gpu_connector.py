@@ -416,3 +416,49 @@ def test_connector_flat_caches_and_misses():
         f"model.layers.{l}.attn": SimpleNamespace(kv_cache=again[l]) for l in range(L)}))
     torch.cuda.synchronize()
     assert all(torch.count_nonzero(t).item() == 0 for t in again)
+
+
+@pytest.mark.parametrize("fmt,bs", [("fp8_e4m3_ph", 32), ("int4_asym_g32", 64),
+                                    ("int4_sym_block", 128), ("fp8_e4m3", 1)])
+def test_slot_paths_other_block_sizes(fmt, bs, monkeypatch):
+    """vLLM blocks of 32, 64, 128 tokens or one token: slots in aligned runs
+    of the entry's page length go through the codec kernels directly (the slot
+    kernel is never called), and the results match the oracle."""
+    from korith_vllm_ext import _paged
+
+    L, H, D = 2, 2, 64
+    S = 4096
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(bs)
+    vals = gen.kv_values((L, 2, S // bs, bs, H, D), D, g, True, dtype)
+    cache = [vals[l].to(DEV) for l in range(L)]
+    page = 128 if fmt == "int4_sym_block" else 16
+    T = 512
+    blocks = gen.block_table(S // max(bs, page), T // max(bs, page), 3).tolist()
+    if bs >= page:
+        slots = _slots_of(blocks, bs, T)
+    else:  # one-token blocks: runs of `page` slots at page-aligned places
+        slots = _slots_of(blocks, page, T)
+
+    def no_slot_kernel(*a, **k):
+        raise AssertionError("slot kernel used on an aligned slot list")
+
+    monkeypatch.setattr(_paged, "scatter_slots", no_slot_kernel)
+    monkeypatch.setattr(_paged, "gather_slots", no_slot_kernel)
+    p = _pool(num_layers=L, default_format=fmt)
+    assert p.put_from_slots("k", cache, slots)
+    got = p.restore_to_tensor("k", target_dtype=dtype)
+    want_l = []
+    for l in range(L):
+        dense = _from_bits(paging.gather_slots(_u16(vals[l]), slots), dtype)
+        want_l.append(_want_dense(fmt, dense, dtype))
+        assert torch.equal(got[l].cpu(), want_l[l])
+    dst_blocks = gen.block_table(S // max(bs, page), T // max(bs, page), 4).tolist()
+    dst = _slots_of(dst_blocks, bs if bs >= page else page, T)
+    target = [torch.full_like(c, -7.25) for c in cache]
+    assert p.restore_to_slots("k", target, dst) == T
+    torch.cuda.synchronize()
+    for l in range(L):
+        want = np.full(tuple(target[l].shape), bits(torch.tensor(-7.25, dtype=dtype)), np.uint16)
+        paging.scatter_slots(want, dst, bits(want_l[l]))
+        assert np.array_equal(bits(target[l]), want), l

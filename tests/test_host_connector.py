@@ -165,3 +165,19 @@ def test_worker_without_gpu_is_inert():
 def test_bad_load_stream_option():
     with pytest.raises(ValueError):
         _conn(load_stream="sideways")
+
+
+def test_token_pages_recut():
+    from korith_vllm_ext import _paged
+
+    x = torch.zeros(2, 8, 32, 2, 64, dtype=torch.bfloat16)
+    v = _paged.cache_view([x])
+    r = _paged.token_pages(v, 16)
+    assert (r.block_size, r.pool_pages, r.page_stride) == (16, 16, 16 * 2 * 64 * 2)
+    assert r.planes == v.planes
+    assert _paged.token_pages(v, 32) is v
+    assert _paged.token_pages(v, 512) is None          # fewer rows than one page
+    nb2 = torch.zeros(8, 2, 32, 2, 64, dtype=torch.bfloat16)
+    pv = _paged.planes_view([nb2[:, 0], nb2[:, 1]])
+    assert _paged.token_pages(pv, 32) is pv            # padded pages: only their own length
+    assert _paged.token_pages(pv, 16) is None
