@@ -17,9 +17,9 @@
 // Dequantisation is folded into the dot products.  With K = s*c + z per
 // (token, 32-dim group):
 //   q.k = sum_g [ s_g * sum_{d in g} q_d c_d + z_g * sum_{d in g} q_d ].
-// Codes enter the matrix cores as the exact bf16 value 16 + c (a nibble
-// dropped into the mantissa of 16.0), so sum q_d (16 + c_d) - 16 sum q_d is
-// folded into the per-group constant: s * C + (z - 16 s) * Qsum.
+// Codes enter the matrix cores as the exact bf16 value 128 + c (the code as
+// the low mantissa byte of 128.0), so sum q_d (128 + c_d) - 128 sum q_d is
+// folded into the per-group constant: s * C + (z - 128 s) * Qsum.
 //
 // MFMA path (v_mfma_f32_16x16x32_bf16, 64 lanes, lane = 16 * hi + lo):
 //  QK^T  computed as S^T[(r,g), t] = sum_k A[(r,g), k] B[k, t] where A holds
@@ -27,7 +27,7 @@
 //        and B the 16 tokens' codes; four k-steps of 32 dims.  Lane (t = lo,
 //        j = hi) then owns C[(r = j, g = 0..3), t] and folds the four groups
 //        itself, so every output is useful.
-//  PV    O[(r,g), d] = sum_t W[(r,g), t] (16 + c_{t,d}) with W = p * s_g(t)
+//  PV    O[(r,g), d] = sum_t W[(r,g), t] (128 + c_{t,d}) with W = p * s_g(t)
 //        split into bf16 hi + lo parts (two MFMAs, ~16-bit weights); the V
 //        pages are stored dim-major in 8x8 tiles, so a lane's B operand (8
 //        tokens of one dim) is one dword of a contiguous 32-byte run.  Only
