@@ -270,6 +270,13 @@ __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
   if (i < n) p[i] = v;
 }
 
+// INT4_SYM save, pass 2: one lane = one 8-element chunk (16 bytes of bf16 in,
+// one 4-byte code word out), so a wave stores 256 contiguous bytes.  Chunk k
+// covers channels (8 k) % head_dim ..+7 and k advances by kThreads, a
+// multiple of head_dim / 8: a lane's 8 channels, and so its scales and
+// reciprocals, stay fixed for the whole page.
+constexpr int kChanUnroll = 4;
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void int4_channel_quant_gather_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
@@ -283,34 +290,40 @@ __global__ __launch_bounds__(kThreads) void int4_channel_quant_gather_kernel(
     return;
   }
   const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
+  const int n8 = (int)(page_elems / 8);
   const uint8_t* __restrict__ src =
       reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
-  uint8_t* __restrict__ codes = reinterpret_cast<uint8_t*>(code_planes[plane]) + j * (page_elems / 2);
-  const int col = sym_col(g), rpi = sym_rpi(g);
-  const uint32_t* lw = ws + (int64_t)(plane / g.pps) * g.head_dim + col * 32;
-  float sc[32], rc[32];
+  uint32_t* __restrict__ codes =
+      reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(code_planes[plane]) + j * (page_elems / 2));
+  const int d0 = (threadIdx.x * 8) % g.head_dim;
+  const uint32_t* lw = ws + (int64_t)(plane / g.pps) * g.head_dim + d0;
+  float sc[8], rc[8];
 #pragma unroll
-  for (int q = 0; q < 32; ++q) {
+  for (int q = 0; q < 8; ++q) {
     sc[q] = fmaxf(u2f(lw[q]), 1e-8f) / kSymMax;  // amf_codec.py:312-313
     rc[q] = 1.0f / sc[q];
   }
-  for (int r = sym_row0(g); r < g.n_rows; r += rpi) {
-    float x[32];
-    load32<DT>(src + elem_bytes<DT>() * ((int64_t)r * g.head_dim + col * 32), x);
-    u32x4 c;
+  for (int base = threadIdx.x; base < n8; base += kThreads * kChanUnroll) {
+    float x[kChanUnroll][8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        float qv = __builtin_rintf(div_rn(x[8 * q + n], sc[8 * q + n], rc[8 * q + n]));
-        qv = fminf(fmaxf(qv, -8.0f), 7.0f);
-        w |= (uint32_t)((int)qv + 8) << (4 * n);
-      }
-      c[q] = w;
+    for (int u = 0; u < kChanUnroll; ++u) {
+      const int k = base + u * kThreads;
+      if (k < n8) load8<DT>(src + (int64_t)k * (8 * elem_bytes<DT>()), x[u]);
     }
-    st_stream(
-        c, reinterpret_cast<u32x4*>(codes + ((int64_t)r * g.head_dim + col * 32) / 2));
+#pragma unroll
+    for (int u = 0; u < kChanUnroll; ++u) {
+      const int k = base + u * kThreads;
+      if (k < n8) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+          float qv = __builtin_rintf(div_rn(x[u][n], sc[n], rc[n]));
+          qv = fminf(fmaxf(qv, -8.0f), 7.0f);
+          w |= (uint32_t)((int)qv + 8) << (4 * n);
+        }
+        st_stream(w, codes + k);
+      }
+    }
   }
 }
 

@@ -637,6 +637,22 @@ def main() -> int:
         log(f"int4 decode: mfma {msd:.4f} ms ({gd:.1f} GB/s), valu {res['valu']:.4f} ms")
         del dc
         torch.cuda.empty_cache()
+        log("reference formats: restore and save at the Llama-3-8B shape")
+        fmts = {}
+        for fmt in ("fp8_e4m3", "int4_sym_block", "int4_sym"):
+            rc = RestoreCase(fmt, 32, 8, 128, 8192, 512, seed=8)
+            r_ms = time_launches(rc.launch.launch, args.steps, args.warmup)
+            sv = rc.save_launch()
+            s_ms = time_launches(sv.launch, args.steps, args.warmup)
+            fmts[fmt] = {"restore_ms": round(r_ms, 5),
+                         "restore_GB/s": round(rc.algo_bytes / r_ms / 1e6, 1),
+                         "save_ms": round(s_ms, 5),
+                         "save_GB/s": round(rc.algo_bytes / s_ms / 1e6, 1),
+                         "algo_bytes": rc.algo_bytes}
+            del sv
+            rc.free()
+        result["reference_formats_llama3_8b_512p"] = fmts
+        log(f"reference formats: {fmts}")
         log("connector: save / load through AMFKVConnector")
         cc = ConnectorCase()
         result["connector"] = cc.run(args.steps, args.warmup)
