@@ -208,6 +208,65 @@ __global__ void fp8_tensor_finalize_kernel(const uint64_t* __restrict__ param_pl
   }
 }
 
+// Per-(page, head) save without a workgroup barrier: a head's bs x head_dim
+// block belongs to one half-wave (32 lanes), each lane holding CPL 8-element
+// chunks of it in registers, so the head's absmax is a 32-lane shuffle
+// reduction and each half-wave quantizes as soon as its own loads land.
+// Chunk c of a head is token c / (head_dim / 8), dims 8 (c % (head_dim / 8))
+// ..+7: 16 consecutive lanes read one 256-byte row (bf16, head_dim 128).
+// A workgroup takes 8 heads per pass.
+template <int DT, int CPL>
+__global__ __launch_bounds__(kThreads) void fp8_ph_quant_gather_kernel(
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
+    const uint64_t* __restrict__ param_planes, PageGeom g, int32_t* err_flag) {
+  const int64_t j = blockIdx.x;
+  const int plane = blockIdx.y;
+  const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
+  if (sp < 0 || sp >= pool) {
+    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    return;
+  }
+  const int H = g.num_heads, D = g.head_dim;
+  const int64_t page_elems = (int64_t)g.n_rows * D;
+  const uint8_t* __restrict__ src =
+      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
+  uint8_t* __restrict__ codes = reinterpret_cast<uint8_t*>(code_planes[plane]) + j * page_elems;
+  float* __restrict__ params = reinterpret_cast<float*>(param_planes[plane]) + j * H;
+  const int lh = threadIdx.x & 31;
+  const int cpr = D >> 3;  // chunks per token row of one head
+  for (int h = (int)(threadIdx.x >> 5); h < H; h += kThreads / 32) {
+    int64_t off[CPL];
+    float x[CPL][8];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lh + 32 * i;
+      off[i] = ((int64_t)(c / cpr) * H + h) * D + (c % cpr) * 8;
+      load8<DT>(src + off[i] * elem_bytes<DT>(), x[i]);
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[i][q]));
+    m = wave_max_xor(m, 32);
+    // scale = max(absmax, 1e-8) / 448, stored per (page, head).
+    const float b = fmaxf(m, 1e-8f) / kFp8Max;
+    const float rb = 1.0f / b;
+    if (lh == 0) params[h] = b;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        x[i][q] = fminf(fmaxf(div_rn(x[i][q], b, rb), -kFp8Max), kFp8Max);
+      u32x2 c;
+      c[0] = f32x4_to_e4m3(x[i]);
+      c[1] = f32x4_to_e4m3(x[i] + 4);
+      st_stream(c, reinterpret_cast<u32x2*>(codes + off[i]));
+    }
+  }
+}
+
 template <bool BF16, bool PER_TENSOR, int R>
 __global__ __launch_bounds__(kThreads) void fp8_quant_gather_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
@@ -463,6 +522,21 @@ extern "C" int amf_fp8_quant_gather(int32_t format, const uint64_t* cache_planes
                    fp8_absmax_kernel<DT><<<agrid, kThreads, 0, s>>>(
                        cache_planes, cache_page_stride, block_ids, pool_pages, n_pages, g, ws,
                        err_flag));
+  }
+  const int64_t head_chunks = (int64_t)(g.n_rows / g.num_heads) * head_dim / 8;
+  const int cpl = (int)(head_chunks / 32);
+  if (!pt && cache_dtype != AMF_DTYPE_F32 && head_chunks % 32 == 0 &&
+      (cpl == 2 || cpl == 4 || cpl == 8 || cpl == 16)) {
+#define AMF_LAUNCH(C)                                                                          \
+  AMF_WITH_DTYPE(cache_dtype, fp8_ph_quant_gather_kernel<DT, C><<<grid, kThreads, 0, s>>>(     \
+                                  cache_planes, cache_page_stride, block_ids, pool_pages,      \
+                                  code_planes, param_planes, g, err_flag))
+    if (cpl == 2) AMF_LAUNCH(2);
+    else if (cpl == 4) AMF_LAUNCH(4);
+    else if (cpl == 8) AMF_LAUNCH(8);
+    else AMF_LAUNCH(16);
+#undef AMF_LAUNCH
+    return check_launch(who);
   }
   if (looped) {
 #define AMF_LAUNCH(T)                                                                         \
