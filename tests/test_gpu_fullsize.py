@@ -67,6 +67,42 @@ def test_restore_fullsize(fmt):
     case.free()
 
 
+@pytest.mark.parametrize("fmt", ["fp8_e4m3_ph", "int4_asym_g32"])
+def test_save_fullsize(fmt):
+    """The save kernels at the benchmark's shapes (bench.py --profile fp8_save /
+    int4_save): blobs of sampled layers equal the oracle's compression of the
+    gathered pages, byte for byte."""
+    if fmt == "fp8_e4m3_ph":
+        case = bench.RestoreCase(fmt, 32, 8, 128, 8192, 512, seed=2)
+    else:
+        case = bench.RestoreCase(fmt, 32, 8, 128, 16384, 2048, seed=3)
+    g = torch.Generator(device="cuda").manual_seed(21)
+    for c in case.cache:
+        c.copy_(torch.randn(c.shape, generator=g, device=DEV).to(torch.bfloat16))
+    case.save_launch().launch()
+    torch.cuda.synchronize()
+    lay = case.layout
+    ids = case.ids.long()
+    for l in (0, 17, case.layers - 1):
+        pages = case.cache[l][:, ids.to(DEV)].cpu()
+        blob = case.blobs[l].cpu()
+        if fmt == "fp8_e4m3_ph":
+            codes, sc = oc.fp8_ph_compress(pages)
+            assert torch.equal(blob[:lay.data_bytes].view(codes.shape), codes), l
+            for p in range(2):
+                got = blob[lay.param_offset(p):lay.param_offset(p) + lay.plane_param_bytes]
+                assert torch.equal(got.view(torch.float32).view(case.pages, case.heads), sc[p]), l
+        else:
+            codes, params = oc.int4_asym_compress(pages)
+            for p in range(2):
+                cb = blob[lay.code_offset(p):lay.code_offset(p) + lay.plane_code_bytes]
+                pb = blob[lay.param_offset(p):lay.param_offset(p) + lay.plane_param_bytes]
+                assert torch.equal(cb.view(codes[p].shape), codes[p]), (l, p)
+                assert torch.equal(pb.view(torch.int32).to(torch.int64).view(params[p].shape) &
+                                   0xFFFFFFFF, params[p]), (l, p)
+    case.free()
+
+
 def _check_decode(dc, algo, seqs):
     out = dc.out.float().cpu().numpy()
     lay = dc.layout
