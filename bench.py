@@ -599,6 +599,13 @@ def main() -> int:
                                   "sample": cb["sample"], "seconds": round(cb["seconds"], 3),
                                   "cpu": platform.processor() or platform.machine(),
                                   "torch": torch.__version__}
+    sv = fp8.save_launch()
+    ms_s = time_launches(sv.launch, args.steps, args.warmup)
+    result["fp8_save"] = {"workload": "fp8_save_llama3_8b", "ms": round(ms_s, 5),
+                          "GB/s": round(fp8.algo_bytes / ms_s / 1e6, 2),
+                          "frac": round(fp8.algo_bytes / ms_s / 1e6 / HBM_PEAK_GBS, 4)}
+    del sv
+    log(f"fp8 save: {ms_s:.4f} ms")
     log("fp8 restore: CompressedVRAMPool API wall clock")
     result["pool_api"] = fp8.pool_api(args.steps, args.warmup)
     log(f"pool api: {result['pool_api']}")
@@ -614,6 +621,13 @@ def main() -> int:
         result["int4_restore"] = {"workload": "int4_restore_llama3_8b", "ms": round(ms4, 5),
                                   "GB/s": round(g4, 2), "frac": round(g4 / HBM_PEAK_GBS, 4),
                                   "algo_bytes": i4.algo_bytes}
+        sv4 = i4.save_launch()
+        ms4s = time_launches(sv4.launch, args.steps, args.warmup)
+        result["int4_save"] = {"workload": "int4_save_llama3_8b", "ms": round(ms4s, 5),
+                               "GB/s": round(i4.algo_bytes / ms4s / 1e6, 2),
+                               "frac": round(i4.algo_bytes / ms4s / 1e6 / HBM_PEAK_GBS, 4)}
+        del sv4
+        log(f"int4 save: {ms4s:.4f} ms")
         i4.free()
         del i4
 
