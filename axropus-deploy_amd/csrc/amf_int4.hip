@@ -395,6 +395,11 @@ __device__ __forceinline__ float param_zero(uint32_t w) {
 //  K: (head, token, group): 16 code bytes + 1 param word -> 32 outputs of a row
 //  V: (head, 8-dim block, token half): 32 code bytes + 8 param words ->
 //     8 tokens x 8 dims.
+#ifndef AMF_ASYM_K_UNROLL
+#define AMF_ASYM_K_UNROLL 4
+#endif
+constexpr int kKUnroll = AMF_ASYM_K_UNROLL;
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
     const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
@@ -418,21 +423,35 @@ __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
   if (!is_v) {
     // Items (token, head, 8-dim block) in cache order: lane k writes the k-th
     // 16-byte vector of the page, reads 4 code bytes and its group's param word.
+    // kKUnroll items per lane have their code and param loads in flight
+    // before any is converted.
     const int kpr = D / 8;  // 8-dim blocks per row
     const int n_items = 16 * H * kpr;
-    for (int it = threadIdx.x; it < n_items; it += kThreads) {
-      const int kk = it % kpr;
-      const int th = it / kpr;  // token * H + head
-      const int t = th / H, h = th % H;
-      const int ht = h * 16 + t;
-      const uint32_t c = ld_stream(
-          reinterpret_cast<const uint32_t*>(codes + (int64_t)ht * (D / 2)) + kk);
-      const uint32_t pw = params[ht * G + (kk >> 2)];
-      const float s = param_scale(pw), z = param_zero(pw);
-      float x[8];
+    for (int it0 = threadIdx.x; it0 < n_items; it0 += kThreads * kKUnroll) {
+      uint32_t c[kKUnroll], pw[kKUnroll];
 #pragma unroll
-      for (int n = 0; n < 8; ++n) x[n] = nib(c, n) * s + z;
-      store8<DT>(out + (int64_t)it * (8 * elem_bytes<DT>()), x);
+      for (int u = 0; u < kKUnroll; ++u) {
+        const int it = it0 + u * kThreads;
+        if (it < n_items) {
+          const int kk = it % kpr;
+          const int th = it / kpr;  // token * H + head
+          const int t = th / H, h = th % H;
+          const int ht = h * 16 + t;
+          c[u] = ld_stream(reinterpret_cast<const uint32_t*>(codes + (int64_t)ht * (D / 2)) + kk);
+          pw[u] = params[ht * G + (kk >> 2)];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kKUnroll; ++u) {
+        const int it = it0 + u * kThreads;
+        if (it < n_items) {
+          const float s = param_scale(pw[u]), z = param_zero(pw[u]);
+          float x[8];
+#pragma unroll
+          for (int n = 0; n < 8; ++n) x[n] = nib(c[u], n) * s + z;
+          store8<DT>(out + (int64_t)it * (8 * elem_bytes<DT>()), x);
+        }
+      }
     }
   } else {
     const int nb = D / 8;
