@@ -484,32 +484,47 @@ __global__ __launch_bounds__(kThreads) void int4_asym_dequant_scatter_kernel(
 
 // Save of one page of a K plane: items (head, token, group) read 64 cache
 // bytes, write 16 code bytes and one param word.
+#ifndef AMF_ASYM_KSAVE_UNROLL
+#define AMF_ASYM_KSAVE_UNROLL 2
+#endif
+constexpr int kKSaveUnroll = AMF_ASYM_KSAVE_UNROLL;
 template <int DT>
 __device__ __forceinline__ void asym_quant_k(const uint8_t* __restrict__ src,
                                              uint8_t* __restrict__ codes,
                                              uint32_t* __restrict__ params, const AsymGeom& g) {
   const int H = g.num_heads, D = g.head_dim, G = g.groups;
   const int n_items = 16 * H * G;
-  for (int it = threadIdx.x; it < n_items; it += kThreads) {
-    // Items in cache order (token, head, group) so the loads are contiguous.
-    const int gi = it % G;
-    const int th = it / G;  // token * H + head
-    const int t = th / H, h = th % H;
-    float x[32];
-    load32<DT>(src + elem_bytes<DT>() * ((int64_t)th * D + 32 * gi), x);
-    const AsymParams p = asym_params(x);
-    u32x4 c;
+  // Items in cache order (token, head, group) so the loads are contiguous;
+  // kKSaveUnroll items per lane are loaded before any is quantized.
+  for (int it0 = threadIdx.x; it0 < n_items; it0 += kThreads * kKSaveUnroll) {
+    float x[kKSaveUnroll][32];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int n = 0; n < 8; ++n) w |= asym_code(x[8 * q + n], p) << (4 * n);
-      c[q] = w;
+    for (int u = 0; u < kKSaveUnroll; ++u) {
+      const int it = it0 + u * kThreads;
+      if (it < n_items)
+        load32<DT>(src + elem_bytes<DT>() * ((int64_t)(it / G) * D + 32 * (it % G)), x[u]);
     }
-    const int ht = h * 16 + t;
-    st_stream(c,
-                                reinterpret_cast<u32x4*>(codes + (int64_t)ht * (D / 2) + 16 * gi));
-    params[ht * G + gi] = asym_param_word(p);
+#pragma unroll
+    for (int u = 0; u < kKSaveUnroll; ++u) {
+      const int it = it0 + u * kThreads;
+      if (it < n_items) {
+        const int gi = it % G;
+        const int th = it / G;  // token * H + head
+        const int t = th / H, h = th % H;
+        const AsymParams p = asym_params(x[u]);
+        u32x4 c;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int n = 0; n < 8; ++n) w |= asym_code(x[u][8 * q + n], p) << (4 * n);
+          c[q] = w;
+        }
+        const int ht = h * 16 + t;
+        st_stream(c, reinterpret_cast<u32x4*>(codes + (int64_t)ht * (D / 2) + 16 * gi));
+        params[ht * G + gi] = asym_param_word(p);
+      }
+    }
   }
 }
 
@@ -519,6 +534,10 @@ __device__ __forceinline__ void asym_quant_k(const uint8_t* __restrict__ src,
 // into LDS first (when it fits); otherwise both phases read the page from
 // global memory, where the second read hits in cache.
 constexpr int kAsymLdsBytes = 64 * 1024;
+#ifndef AMF_ASYM_STAGE_UNROLL
+#define AMF_ASYM_STAGE_UNROLL 8
+#endif
+constexpr int kStageUnroll = AMF_ASYM_STAGE_UNROLL;
 
 template <int DT, bool STAGED>
 __device__ __forceinline__ void asym_quant_v(const uint8_t* __restrict__ src,
@@ -530,8 +549,20 @@ __device__ __forceinline__ void asym_quant_v(const uint8_t* __restrict__ src,
   const int page_bytes = STAGED ? 16 * H * D * ES : 0;
   // phase 0: page -> LDS (cache layout)
   if (STAGED) {
-    for (int o = threadIdx.x * 16; o < page_bytes; o += kThreads * 16)
-      *reinterpret_cast<u32x4*>(lds + o) = *reinterpret_cast<const u32x4*>(src + o);
+    // kStageUnroll vectors per lane in flight before they are stored to LDS.
+    for (int o0 = threadIdx.x * 16; o0 < page_bytes; o0 += kThreads * 16 * kStageUnroll) {
+      u32x4 v[kStageUnroll];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int o = o0 + u * kThreads * 16;
+        if (o < page_bytes) v[u] = *reinterpret_cast<const u32x4*>(src + o);
+      }
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int o = o0 + u * kThreads * 16;
+        if (o < page_bytes) *reinterpret_cast<u32x4*>(lds + o) = v[u];
+      }
+    }
   }
   const uint8_t* data = STAGED ? lds : src;
   float* s_mn = reinterpret_cast<float*>(lds + page_bytes);          // [H][G][16]
