@@ -258,17 +258,13 @@ __device__ __forceinline__ int64_t split_page(const SplitPages& sp, int pi, bool
 
 // ============================================================== MFMA path ==
 
-// One 32-token chunk of the MFMA kernel: QK^T, online softmax, PV.  FULL:
-// all 32 tokens are inside the context and both pages are valid.
+// One 32-token chunk of the MFMA kernel: QK^T, online softmax, PV.
 #ifndef AMF_DECODE_RESCALE_SLACK
 #define AMF_DECODE_RESCALE_SLACK 8.0f
 #endif
-#ifndef AMF_DECODE_FULL_FAST
-#define AMF_DECODE_FULL_FAST 0
-#endif
 constexpr float kRescaleSlack = AMF_DECODE_RESCALE_SLACK;  // log2 units
 
-template <int R, bool QBF16, bool FULL>
+template <int R, bool QBF16>
 __device__ __forceinline__ void mfma_chunk(
     const DecodeArgs& a, const ChunkLoads& cur, const bool (&pok)[2], int c0, int tok_end, int lo,
     int hi, const u32x4 (&qa_hi)[(R + 3) / 4][4], const u32x4 (&qa_lo)[(R + 3) / 4][4],
@@ -294,7 +290,7 @@ __device__ __forceinline__ void mfma_chunk(
       ks[gi] = pscale(kpar[u][gi]);
       kz[gi] = pzero(kpar[u][gi]) - kCodeBias * ks[gi];
     }
-    const bool valid = FULL || (pok[u] && (c0 + u * kBS + lo) < tok_end);
+    const bool valid = pok[u] && (c0 + u * kBS + lo) < tok_end;
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
       f32x4 cacc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -358,7 +354,7 @@ __device__ __forceinline__ void mfma_chunk(
     float cs = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const bool valid = FULL || (vpage_ok && (c0 + 8 * hi + e) < tok_end);
+      const bool valid = vpage_ok && (c0 + 8 * hi + e) < tok_end;
       const uint32_t pwe = valid ? pw[e] : 0u;
       const float sv = pscale(pwe);
       wk[k_of_nib(e)] = pv[e] * sv;
@@ -477,14 +473,8 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     pg_n[0] = split_page(spg, cn / kBS, &pok_n[0]);
     pg_n[1] = split_page(spg, cn / kBS + 1, &pok_n[1]);
     nxt = issue_chunk(a, pg_n[0], pg_n[1], h, lo, hi);
-    // A chunk of 32 valid tokens on valid pages (the common case) skips the
-    // per-token masks.
-    if (AMF_DECODE_FULL_FAST && pok[0] && pok[1] && c0 + 32 <= tok_end)
-      mfma_chunk<R, QBF16, true>(a, cur, pok, c0, tok_end, lo, hi, qa_hi, qa_lo, qsum, m_run,
-                                 l_run, corr, acc, p_lds);
-    else
-      mfma_chunk<R, QBF16, false>(a, cur, pok, c0, tok_end, lo, hi, qa_hi, qa_lo, qsum, m_run,
-                                  l_run, corr, acc, p_lds);
+    mfma_chunk<R, QBF16>(a, cur, pok, c0, tok_end, lo, hi, qa_hi, qa_lo, qsum, m_run, l_run,
+                         corr, acc, p_lds);
   }
 
   // ---- write the split's partial (unnormalised O, m, l) ----
