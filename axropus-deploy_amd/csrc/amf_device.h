@@ -1,10 +1,11 @@
 // amf_device.h - scalar conversion helpers shared by the gfx950 kernels.
 //
-// Every helper is plain integer/float code so that the same definitions also
-// compile as host C++ (g++), which is how the CPU test suite checks them
-// against independent encoders.  Rounding is fixed by the functions
-// themselves; kernels are compiled with -ffp-contract=off so that no
-// multiply/add pair is silently fused.
+// Every helper is plain integer/float code, so the same definitions also
+// compile as host C++ (g++).  The GPU tests check them against the oracle's
+// independent encoders through the kernels and libamf_selftest.so, which also
+// sweeps the e4m3 encoder against gfx950's conversion instruction.  Rounding
+// is fixed by the functions themselves; kernels are compiled with
+// -ffp-contract=off so that no multiply/add pair is silently fused.
 #pragma once
 
 #include <stdint.h>

@@ -18,8 +18,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "amf_hip.h")
 
 
-def header_functions():
-    text = open(HEADER).read()
+def header_functions(header: str = HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return set(re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(amf_\w+)\s*\(", text, flags=re.M))
 
@@ -51,6 +51,20 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
     fns = header_functions()
     assert fns == set(amf_hip.SIGNATURES), fns ^ set(amf_hip.SIGNATURES)
     raw = ctypes.CDLL(amf_hip.LIB_PATH)
+    for f in fns:
+        assert hasattr(raw, f), f
+
+
+def test_selftest_library_exports_its_header():
+    """libamf_selftest.so (the encoder checks the GPU tests run) exports what
+    include/amf_selftest.h declares, and nothing of it is in the drop-in ABI."""
+    path = os.path.join(os.path.dirname(amf_hip.LIB_PATH), "libamf_selftest.so")
+    if not os.path.exists(path):
+        pytest.fail(f"{path} missing: run __graft_entry__.build()")
+    fns = header_functions(os.path.join(ROOT, "include", "amf_selftest.h"))
+    assert fns == {"amf_selftest_e4m3_sweep", "amf_selftest_e4m3_encode"}
+    assert not fns & header_functions()
+    raw = ctypes.CDLL(path)
     for f in fns:
         assert hasattr(raw, f), f
 
