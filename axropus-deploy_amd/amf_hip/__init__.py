@@ -29,6 +29,7 @@ ERR_WORKSPACE = -4
 
 ERRFLAG_BLOCK_RANGE = 1
 ERRFLAG_CONTEXT = 2
+ERRFLAG_SYNC = 4
 
 # element types (same numbering as the AMFK header dtype tag)
 DTYPE_F16 = 0

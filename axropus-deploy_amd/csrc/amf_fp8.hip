@@ -11,6 +11,10 @@
 // 16-element column chunk (tid % (head_dim/16)) of rows tid / (head_dim/16),
 // + rows_per_iter, ...  Code chunks are 16-byte loads/stores, cache chunks two
 // 16-byte vectors.
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "amf_internal.h"
 #include "amf_kernel_util.h"
 
@@ -205,6 +209,264 @@ __global__ void fp8_tensor_finalize_kernel(const uint64_t* __restrict__ param_pl
     sc[1] = s;
     sc[2] = 1.0f;
     sc[3] = 1.0f;
+  }
+}
+
+// Per-tensor save in one read of the cache.  The two-pass form (absmax
+// kernel, then a quantize kernel that reads every page again) moves two
+// reads and a write through HBM.  Here a cooperative grid (every workgroup
+// resident) walks the scale groups in order and keeps its share of a group
+// in registers from the load to the store: the group's absmax is one atomic
+// max per workgroup into ws[group], a per-group arrival counter says when
+// every workgroup has contributed, and only then are the held values
+// quantized and stored.  Two register buffers alternate, so the next group's
+// loads are in flight while a workgroup waits on the current group's count.
+// The exchange is a two-level tree, because device-scope atomics on one
+// cache line serialize (one line for the whole grid cost about 20 us per
+// group): workgroup b reports to cluster b % kCoopClusters, each cluster's
+// last arrival forwards the cluster's max to the group's root line, and the
+// root's last arrival writes the group's max with a ready bit into every
+// cluster's line, where that cluster's workgroups poll for it.  Each
+// cluster and root keeps its words on its own 128-byte line.
+// Workgroup b holds pages b, b + G, b + 2G, ... of a group (G workgroups,
+// at most kCoopChunks / CPT pages each); its lanes hold CPT 16-byte chunks
+// of each page (tid + 256 m), so page addresses are workgroup-uniform.  The
+// host takes this path only when a group fits the grid; others take the
+// two-pass kernels.
+constexpr int kCoopChunks = 16;
+constexpr int kCoopThreads = 256;
+constexpr uint32_t kCoopSpinLimit = 1u << 20;
+constexpr int kCoopClusters = kFp8CoopClusters;
+constexpr int kLineWords = kFp8CoopLineWords;  // one 128-byte line
+constexpr uint32_t kReady = 0x80000000u;  // above every non-negative float's bits
+
+struct CoopArgs {
+  const uint64_t* cache_planes;
+  int64_t cache_stride;
+  const int32_t* block_ids;
+  int64_t pool;
+  const uint64_t* code_planes;
+  int64_t n_pages;
+  int64_t group_pages;  // pps * n_pages
+  int64_t page_elems;
+  int pps;
+  int n_groups;
+  int ppw;              // pages per workgroup per group
+  uint32_t* ws;         // [n_groups] absmax bits, written by each group's root
+  // Per group, kCoopClusters + 1 lines, zeroed before the launch.  Cluster
+  // line k: [0] arrivals, [1] max bits, [2] the group's max | kReady once
+  // complete.  Root line: [0] clusters complete, [1] max bits.
+  uint32_t* sync;
+  int32_t* err_flag;
+};
+
+__device__ __forceinline__ uint32_t* coop_line(const CoopArgs& a, int gi, int k) {
+  return a.sync + ((int64_t)gi * (kCoopClusters + 1) + k) * kLineWords;
+}
+
+// Page i of this workgroup in group gi: its plane and gathered position,
+// whether it exists, and whether it also has an in-range block id (sp).
+struct CoopPage {
+  bool exists;
+  bool ok;
+  int plane;
+  int64_t j;
+  int64_t sp;
+};
+
+__device__ __forceinline__ CoopPage coop_page(const CoopArgs& a, int gi, int i) {
+  CoopPage r;
+  const int64_t pg = blockIdx.x + (int64_t)i * gridDim.x;
+  r.exists = i < a.ppw && pg < a.group_pages;
+  r.ok = r.exists;
+  r.plane = 0;
+  r.j = 0;
+  r.sp = -1;
+  if (r.exists) {
+    const int pl = (int)(pg / a.n_pages);
+    r.plane = gi * a.pps + pl;
+    r.j = pg - (int64_t)pl * a.n_pages;
+    r.sp = a.block_ids ? (int64_t)a.block_ids[r.j] : r.j;
+    r.ok = r.sp >= 0 && r.sp < a.pool;
+  }
+  return r;
+}
+
+// Loads the workgroup's pages of group gi; absent pages and pages whose
+// block id is out of range read as zero (and are never stored).
+template <int CPT>
+__device__ __forceinline__ void coop_load(const CoopArgs& a, int gi, u32x4 (&buf)[kCoopChunks]) {
+#pragma unroll
+  for (int i = 0; i < kCoopChunks / CPT; ++i) {
+    const CoopPage q = coop_page(a, gi, i);
+    if (q.ok) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(
+          reinterpret_cast<const uint8_t*>(a.cache_planes[q.plane]) + q.sp * a.cache_stride);
+#pragma unroll
+      for (int m = 0; m < CPT; ++m)
+        buf[i * CPT + m] = ld_stream(src + threadIdx.x + kCoopThreads * m);
+    } else {
+#pragma unroll
+      for (int m = 0; m < CPT; ++m) buf[i * CPT + m] = u32x4{0u, 0u, 0u, 0u};
+      if (q.exists && threadIdx.x == 0 && a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    }
+  }
+}
+
+// The absmax works on the 16-bit patterns: for non-NaN values |x| orders as
+// its bits with the sign cleared, and NaN patterns (above the infinity
+// pattern) are dropped, as fmaxf drops them in the two-pass kernel.  Not
+// converting to fp32 here also keeps the compiler from holding converted
+// copies of the buffer until the store.
+template <int DT>
+__device__ __forceinline__ uint32_t absmax_bits16(const u32x4& v, uint32_t m) {
+  constexpr uint32_t kInf = DT == AMF_DTYPE_BF16 ? 0x7F80u : 0x7C00u;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t lo = v[q] & 0x7FFFu, hi = (v[q] >> 16) & 0x7FFFu;
+    lo = lo > kInf ? 0u : lo;
+    hi = hi > kInf ? 0u : hi;
+    m = max(m, max(lo, hi));
+  }
+  return m;
+}
+
+// Reports the buffer's absmax for group gi.  Lane 0 folds it into its
+// cluster's max, waits for that atomic to complete, then counts itself in;
+// each atomic is device-scope, performed where every XCD sees it.  The
+// cluster's last arrival (its count returns cluster size - 1, so every other
+// member's max is already in) forwards the cluster max to the root the same
+// way, and the root's last arrival publishes the group's max to ws[gi] and
+// to every cluster line.  The codes a workgroup stored need not be visible
+// to others, so no release fence (an L2 write-back) is taken.
+template <int DT>
+__device__ __forceinline__ void coop_arrive(const CoopArgs& a, int gi,
+                                            const u32x4 (&buf)[kCoopChunks], uint32_t* s_max) {
+  uint32_t mb = 0;
+#pragma unroll
+  for (int k = 0; k < kCoopChunks; ++k) mb = absmax_bits16<DT>(buf[k], mb);
+  float m;
+  if constexpr (DT == AMF_DTYPE_BF16)
+    m = u2f(mb << 16);
+  else
+    m = (float)__builtin_bit_cast(_Float16, (uint16_t)mb);
+  m = wave_max_xor(m, 64);
+  if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = f2u(m);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t b = s_max[0];
+#pragma unroll
+    for (int w = 1; w < kCoopThreads / 64; ++w) b = b > s_max[w] ? b : s_max[w];
+    const int G = (int)gridDim.x;
+    const int k = (int)blockIdx.x % kCoopClusters;
+    const int n_clusters = G < kCoopClusters ? G : kCoopClusters;
+    const uint32_t members = (uint32_t)((G - k + kCoopClusters - 1) / kCoopClusters);
+    uint32_t* cl = coop_line(a, gi, k);
+    __hip_atomic_fetch_max(cl + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the max has completed before the count moves
+    if (__hip_atomic_fetch_add(cl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        members - 1) {
+      const uint32_t cm = __hip_atomic_load(cl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uint32_t* root = coop_line(a, gi, kCoopClusters);
+      __hip_atomic_fetch_max(root + 1, cm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      if (__hip_atomic_fetch_add(root, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          (uint32_t)n_clusters - 1) {
+        const uint32_t gm =
+            __hip_atomic_load(root + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_max(a.ws + gi, gm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int c = 0; c < n_clusters; ++c)
+          __hip_atomic_store(coop_line(a, gi, c) + 2, gm | kReady, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+// Waits (lane 0, bounded) for group gi's max on this workgroup's cluster
+// line and returns it to the whole workgroup.  Every workgroup of a
+// cooperative launch is resident, so the max arrives; the bound only keeps a
+// broken launch from spinning forever.  A workgroup whose wait runs out
+// raises AMF_ERRFLAG_SYNC, waits no more (no workgroup spins longer than one
+// bound in a launch), and raises the group's absmax slot to +inf, so the
+// scale written for that group is infinite and a restore of it yields
+// inf/NaN rather than plausible values.
+__device__ __forceinline__ uint32_t coop_wait(const CoopArgs& a, int gi, uint32_t* s_bits,
+                                              bool& gave_up) {
+  if (threadIdx.x == 0) {
+    const uint32_t* go = coop_line(a, gi, (int)blockIdx.x % kCoopClusters) + 2;
+    uint32_t v = __hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t spins = 0;
+    while (!gave_up && !(v & kReady)) {
+      if (++spins > kCoopSpinLimit) {
+        if (a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_SYNC);
+        gave_up = true;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      v = __hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!(v & kReady))
+      __hip_atomic_fetch_max(a.ws + gi, 0x7F800000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_bits = v & ~kReady;
+  }
+  __syncthreads();
+  const uint32_t bits = *s_bits;
+  __syncthreads();  // s_bits is reused by the next group
+  return bits;
+}
+
+template <int DT, int CPT>
+__device__ __forceinline__ void coop_store(const CoopArgs& a, int gi,
+                                           const u32x4 (&buf)[kCoopChunks], uint32_t amax_bits) {
+  const float am = fmaxf(u2f(amax_bits), tensor_floor<DT>());
+  const float tdiv = (am == 0.0f) ? 1e-12f : am / kFp8Max;
+  const float trcp = 1.0f / tdiv;
+#pragma unroll
+  for (int i = 0; i < kCoopChunks / CPT; ++i) {
+    const CoopPage q = coop_page(a, gi, i);
+    if (!q.ok) continue;
+    u32x2* codes = reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(a.code_planes[q.plane]) +
+                                            q.j * a.page_elems);
+#pragma unroll
+    for (int m = 0; m < CPT; ++m) {
+      float x[8];
+      unpack8<DT == AMF_DTYPE_BF16>(buf[i * CPT + m], x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        x[e] = fminf(fmaxf(div_rn(x[e], tdiv, trcp), -kFp8Max), kFp8Max);
+      u32x2 cw;
+      cw[0] = f32x4_to_e4m3(x);
+      cw[1] = f32x4_to_e4m3(x + 4);
+      st_stream(cw, codes + threadIdx.x + kCoopThreads * m);
+    }
+  }
+}
+
+template <int DT, int CPT>
+__global__ __launch_bounds__(kCoopThreads) void fp8_tensor_coop_kernel(CoopArgs a) {
+  __shared__ uint32_t s_max[kCoopThreads / 64];
+  __shared__ uint32_t s_bits;
+  bool gave_up = false;  // lane 0's: a wait ran out of its bound
+  u32x4 b0[kCoopChunks], b1[kCoopChunks];
+  const int ng = a.n_groups;
+  coop_load<CPT>(a, 0, b0);
+  coop_arrive<DT>(a, 0, b0, s_max);
+  if (ng > 1) coop_load<CPT>(a, 1, b1);
+  // Groups in pairs so that each buffer is a fixed register array.  A group
+  // is reported as soon as the previous group's max is known (its loads were
+  // issued before that wait), ahead of the previous group's stores, so the
+  // report never waits on store completion.  Every workgroup takes the same
+  // branches (they depend on n_groups only).
+  for (int gi = 0; gi < ng; gi += 2) {
+    const uint32_t m0 = coop_wait(a, gi, &s_bits, gave_up);
+    if (gi + 1 < ng) coop_arrive<DT>(a, gi + 1, b1, s_max);
+    coop_store<DT, CPT>(a, gi, b0, m0);
+    if (gi + 2 < ng) coop_load<CPT>(a, gi + 2, b0);
+    if (gi + 1 >= ng) break;
+    const uint32_t m1 = coop_wait(a, gi + 1, &s_bits, gave_up);
+    if (gi + 2 < ng) coop_arrive<DT>(a, gi + 2, b0, s_max);
+    coop_store<DT, CPT>(a, gi + 1, b1, m1);
+    if (gi + 3 < ng) coop_load<CPT>(a, gi + 3, b1);
   }
 }
 
@@ -446,6 +708,101 @@ int make_geom(const char* who, int32_t block_size, int32_t num_heads, int32_t he
   return ok();
 }
 
+// The cooperative kernel for a cache dtype and chunks per page row (CPT),
+// or nullptr for combinations it does not cover.
+const void* coop_kernel(int dt, int cpt) {
+#define AMF_COOP(D, C) reinterpret_cast<const void*>(&fp8_tensor_coop_kernel<D, C>)
+#define AMF_COOP_CPT(D)                                               \
+  switch (cpt) {                                                      \
+    case 1: return AMF_COOP(D, 1);                                    \
+    case 2: return AMF_COOP(D, 2);                                    \
+    case 4: return AMF_COOP(D, 4);                                    \
+    case 8: return AMF_COOP(D, 8);                                    \
+    case 16: return AMF_COOP(D, 16);                                  \
+    default: return nullptr;                                          \
+  }
+  if (dt == AMF_DTYPE_BF16) { AMF_COOP_CPT(AMF_DTYPE_BF16) }
+  if (dt == AMF_DTYPE_F16) { AMF_COOP_CPT(AMF_DTYPE_F16) }
+  return nullptr;
+#undef AMF_COOP_CPT
+#undef AMF_COOP
+}
+
+// Workgroups of a cooperative kernel that the current device keeps resident
+// at once (0: no cooperative launch).  Queried once per (device, kernel).
+int coop_blocks(const void* fn) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, fn);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int coop = 0, cus = 0, per_cu = 0;
+  hipError_t e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kCoopThreads, 0);
+  if (e != hipSuccess) (void)hipGetLastError();
+  const int blocks = (e == hipSuccess && coop) ? per_cu * cus : 0;
+  cache[key] = blocks;
+  return blocks;
+}
+
+// Smallest scale group (bytes of cache read) worth the cooperative path: a
+// smaller group's wait costs more than its second read.
+constexpr int64_t kCoopMinGroupBytes = 4ll << 20;
+constexpr int kCoopNotTaken = 1;
+
+// Per-tensor save through fp8_tensor_coop_kernel when the device supports a
+// cooperative launch, a page row of chunks maps onto the workgroup (the
+// page's 16-byte chunks are 256 * CPT, CPT a power of two <= kCoopChunks)
+// and a scale group fits the grid.  Returns AMF_OK after the launch,
+// kCoopNotTaken to leave the call to the two-pass kernels (nothing
+// launched), or an error code.  ws must hold the zeroed absmax slots and
+// arrival counters.
+int try_tensor_coop(int32_t dt, const uint64_t* cache_planes, int64_t cache_page_stride,
+                    const int32_t* block_ids, int64_t pool_pages, const uint64_t* code_planes,
+                    int64_t n_pages, const PageGeom& g, int n_groups, uint32_t* ws,
+                    int32_t* err_flag, hipStream_t s) {
+  if (!aligned16(cache_page_stride)) return kCoopNotTaken;
+  const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
+  const int64_t chunks_pp = page_elems / 8;  // head_dim % 16 == 0: whole 16-byte chunks
+  if (chunks_pp % kCoopThreads != 0) return kCoopNotTaken;
+  const int cpt = (int)(chunks_pp / kCoopThreads);
+  const void* fn = coop_kernel(dt, cpt);
+  if (!fn) return kCoopNotTaken;
+  const int64_t group_pages = (int64_t)g.pps * n_pages;
+  if (group_pages * chunks_pp * 16 < kCoopMinGroupBytes) return kCoopNotTaken;
+  const int blocks = coop_blocks(fn);
+  if (blocks <= 0) return kCoopNotTaken;
+  const int64_t ppw = (group_pages + blocks - 1) / blocks;
+  if (ppw > kCoopChunks / cpt) return kCoopNotTaken;
+  CoopArgs a;
+  a.cache_planes = cache_planes;
+  a.cache_stride = cache_page_stride;
+  a.block_ids = block_ids;
+  a.pool = pool_pages;
+  a.code_planes = code_planes;
+  a.n_pages = n_pages;
+  a.group_pages = group_pages;
+  a.page_elems = page_elems;
+  a.pps = g.pps;
+  a.n_groups = n_groups;
+  a.ppw = (int)ppw;
+  a.ws = ws;
+  a.sync = ws + fp8_tensor_sync_offset(n_groups);
+  a.err_flag = err_flag;
+  void* args[] = {&a};
+  const hipError_t e =
+      hipLaunchCooperativeKernel(fn, dim3((unsigned)blocks), dim3(kCoopThreads), args, 0, s);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return kCoopNotTaken;
+  }
+  return ok();
+}
+
 }  // namespace
 
 extern "C" int amf_fp8_dequant_scatter(int32_t format, const uint64_t* code_planes,
@@ -514,7 +871,17 @@ extern "C" int amf_fp8_quant_gather(int32_t format, const uint64_t* cache_planes
   uint32_t* ws = reinterpret_cast<uint32_t*>(workspace);
   const int n_groups = n_planes / g.pps;
   if (pt) {
-    fill_u32_kernel<<<(n_groups + 255) / 256, 256, 0, s>>>(ws, n_groups, 0u);
+    // ws: n_groups absmax slots, then the single-read kernel's cluster lines.
+    const int n_words = (int)fp8_tensor_workspace_words(n_groups);
+    fill_u32_kernel<<<(n_words + 255) / 256, 256, 0, s>>>(ws, n_words, 0u);
+    rc = try_tensor_coop(cache_dtype, cache_planes, cache_page_stride, block_ids, pool_pages,
+                         code_planes, n_pages, g, n_groups, ws, err_flag, s);
+    if (rc != kCoopNotTaken) {
+      if (rc != AMF_OK) return rc;
+      AMF_WITH_DTYPE(cache_dtype, fp8_tensor_finalize_kernel<DT>
+                     <<<(n_planes + 255) / 256, 256, 0, s>>>(param_planes, ws, n_planes, g.pps));
+      return check_launch(who);
+    }
     const int64_t per_plane = std::max<int64_t>(
         1, std::min<int64_t>(n_pages, (kAbsBlocks + n_planes - 1) / n_planes));
     dim3 agrid((unsigned)per_plane, (unsigned)n_planes);

@@ -46,6 +46,18 @@ inline int cache_elem_bytes(int32_t dtype) {
     }                                                                 \
   } while (0)
 
+// Per-tensor FP8 save workspace (words): the n_groups absmax slots, then,
+// on a 128-byte line boundary, kFp8CoopClusters + 1 lines per group for the
+// single-read kernel's cross-workgroup exchange.
+constexpr int kFp8CoopClusters = 32;
+constexpr int kFp8CoopLineWords = 32;
+inline int64_t fp8_tensor_sync_offset(int64_t n_groups) {
+  return (n_groups + kFp8CoopLineWords - 1) / kFp8CoopLineWords * kFp8CoopLineWords;
+}
+inline int64_t fp8_tensor_workspace_words(int64_t n_groups) {
+  return fp8_tensor_sync_offset(n_groups) + n_groups * (kFp8CoopClusters + 1) * kFp8CoopLineWords;
+}
+
 // Common validation of the paged-geometry arguments of the codec entry points.
 int check_codec_geometry(const char* who, const uint64_t* cache_planes,
                          int64_t cache_page_stride, int32_t cache_dtype,

@@ -70,7 +70,7 @@ extern "C" int64_t amf_quant_workspace_bytes(int32_t format, int32_t n_planes,
   if (n_planes <= 0 || planes_per_scale <= 0) return 0;
   const int64_t n_groups = (n_planes + planes_per_scale - 1) / planes_per_scale;
   switch (format) {
-    case AMF_FMT_FP8_E4M3: return n_groups * (int64_t)sizeof(float);
+    case AMF_FMT_FP8_E4M3: return amf::fp8_tensor_workspace_words(n_groups) * (int64_t)sizeof(float);
     case AMF_FMT_INT4_SYM: return n_groups * (int64_t)head_dim * (int64_t)sizeof(float);
     default: return 0;
   }

@@ -507,6 +507,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--profile", choices=["fp8_restore", "int4_restore", "fp8_save", "int4_save",
+                                          "fp8_tensor_save",
                                           "fp8_restore_70b", "decode_70b", "decode_mfma",
                                           "decode_valu", "copy", "slot_copy"], default=None,
                     help="run only this kernel loop (for rocprofv3)")
@@ -558,10 +559,12 @@ def main() -> int:
             ms = time_launches(lambda: case.launch(amf_hip.DECODE_MFMA), args.steps, args.warmup)
             log(f"{args.profile}: {ms:.4f} ms/call, {case.algo_bytes / ms / 1e6:.1f} GB/s")
             return 0
-        if args.profile in ("fp8_restore", "int4_restore", "fp8_save", "int4_save"):
-            fmt = "fp8_e4m3_ph" if args.profile.startswith("fp8") else "int4_asym_g32"
-            case = (RestoreCase(fmt, 32, 8, 128, 8192, 512, 2) if fmt == "fp8_e4m3_ph"
-                    else RestoreCase(fmt, 32, 8, 128, 16384, 2048, 3))
+        if args.profile in ("fp8_restore", "int4_restore", "fp8_save", "int4_save",
+                            "fp8_tensor_save"):
+            fmt = ("fp8_e4m3" if args.profile == "fp8_tensor_save" else
+                   "fp8_e4m3_ph" if args.profile.startswith("fp8") else "int4_asym_g32")
+            case = (RestoreCase(fmt, 32, 8, 128, 16384, 2048, 3) if fmt == "int4_asym_g32"
+                    else RestoreCase(fmt, 32, 8, 128, 8192, 512, 2))
             launch = case.launch if args.profile.endswith("restore") else case.save_launch()
             ms = time_launches(launch.launch, args.steps, args.warmup)
             log(f"{args.profile}: {ms:.4f} ms/launch, {case.algo_bytes / ms / 1e6:.1f} GB/s")

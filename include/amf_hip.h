@@ -64,6 +64,7 @@ extern "C" {
 /* bits ORed into *err_flag by kernels */
 #define AMF_ERRFLAG_BLOCK_RANGE 1    /* a block id was outside [0, pool_pages) */
 #define AMF_ERRFLAG_CONTEXT     2    /* a context length exceeded its block table */
+#define AMF_ERRFLAG_SYNC        4    /* a cross-workgroup wait gave up (that call's output is invalid) */
 
 /* ---- element types: same numbering as the AMFK header dtype field
  *      (core/amf_direct_kv.h AmfKvDtype; amf_kv_manager.py:60-64) --------- */
@@ -135,8 +136,10 @@ int amf_abi_version(void);
 const char* amf_last_error(void);
 
 /* Bytes of fp32 workspace that amf_*_quant_gather needs for `format`
- * (cross-page reductions of AMF_FMT_FP8_E4M3 and AMF_FMT_INT4_SYM: one slot,
- * or head_dim slots, per scale group); 0 for formats reduced within a page. */
+ * (cross-page reductions: AMF_FMT_FP8_E4M3 one absmax word per scale group,
+ * padded to a 128-byte line, then 33 lines per group that the single-read
+ * save exchanges its partial maxima through; AMF_FMT_INT4_SYM head_dim
+ * slots per group); 0 for formats reduced within a page. */
 int64_t amf_quant_workspace_bytes(int32_t format, int32_t n_planes, int32_t planes_per_scale,
                                   int32_t head_dim);
 
@@ -190,7 +193,13 @@ int amf_kv_scatter_slots(const uint64_t* in_planes, int64_t in_row_stride,
  * value).  planes_per_scale (>= 1, dividing n_planes) groups planes for the
  * per-tensor format and is ignored otherwise.  workspace: device fp32
  * buffer of amf_quant_workspace_bytes() bytes (may be NULL when that is 0);
- * its contents on entry do not matter.
+ * its contents on entry do not matter.  The per-tensor format reads the cache
+ * once through a cooperative launch when the device supports it and a scale
+ * group (planes_per_scale planes of n_pages pages, at least 4 MiB) fits the
+ * resident grid, and twice (absmax kernel, then quantize kernel) otherwise;
+ * both give the same bytes.  A cooperative wait that gives up (never in a
+ * correct launch) raises AMF_ERRFLAG_SYNC and writes an infinite scale for
+ * its group.
  * Replaces compressed_vram_pool.py:481-508 with FP8E4M3Codec.compress
  * (amf_codec.py:186-209). */
 int amf_fp8_quant_gather(int32_t format,

@@ -80,7 +80,7 @@ def test_constants_match_header(lib):
 
 def test_workspace_queries(lib):
     d = header_defines()
-    assert amf_hip.quant_workspace_bytes(d["AMF_FMT_FP8_E4M3"], 64, 2, 128) == 32 * 4
+    assert amf_hip.quant_workspace_bytes(d["AMF_FMT_FP8_E4M3"], 64, 2, 128) == (32 + 32 * 33 * 32) * 4
     assert amf_hip.quant_workspace_bytes(d["AMF_FMT_INT4_SYM"], 4, 4, 128) == 128 * 4
     assert amf_hip.quant_workspace_bytes(d["AMF_FMT_FP8_E4M3_PH"], 64, 1, 128) == 0
     a = amf_hip.decode_workspace_bytes(32, 32, 8, 128, 32768)

@@ -67,12 +67,13 @@ def test_restore_fullsize(fmt):
     case.free()
 
 
-@pytest.mark.parametrize("fmt", ["fp8_e4m3_ph", "int4_asym_g32"])
+@pytest.mark.parametrize("fmt", ["fp8_e4m3_ph", "fp8_e4m3", "int4_asym_g32"])
 def test_save_fullsize(fmt):
     """The save kernels at the benchmark's shapes (bench.py --profile fp8_save /
-    int4_save): blobs of sampled layers equal the oracle's compression of the
-    gathered pages, byte for byte."""
-    if fmt == "fp8_e4m3_ph":
+    int4_save; the per-tensor format at the same shape takes the single-read
+    cooperative kernel): blobs of sampled layers equal the oracle's
+    compression of the gathered pages, byte for byte."""
+    if fmt in ("fp8_e4m3_ph", "fp8_e4m3"):
         case = bench.RestoreCase(fmt, 32, 8, 128, 8192, 512, seed=2)
     else:
         case = bench.RestoreCase(fmt, 32, 8, 128, 16384, 2048, seed=3)
@@ -92,6 +93,11 @@ def test_save_fullsize(fmt):
             for p in range(2):
                 got = blob[lay.param_offset(p):lay.param_offset(p) + lay.plane_param_bytes]
                 assert torch.equal(got.view(torch.float32).view(case.pages, case.heads), sc[p]), l
+        elif fmt == "fp8_e4m3":
+            codes, scale = oc.fp8_tensor_compress(pages)
+            assert torch.equal(blob[:lay.data_bytes].view(codes.shape), codes), l
+            side = blob[lay.scale_offset:lay.scale_offset + 16].view(torch.float32)
+            assert torch.equal(side, oc.fp8_sidecar(scale)), l
         else:
             codes, params = oc.int4_asym_compress(pages)
             for p in range(2):

@@ -161,6 +161,44 @@ def test_fp8_tensor_format_bitexact(dtype, geom):
     _check_restored(target, dst_ids, want, dtype, geom)
 
 
+# Scale groups of at least 4 MiB whose pages are whole multiples of 256
+# 16-byte chunks take the single-read cooperative kernel: an odd group count
+# (the last group has no partner buffer), one page per workgroup (CPT 8) and
+# several pages per workgroup (CPT 1).
+COOP_CASES = [
+    pytest.param(torch.bfloat16, dict(L=3, pool=512, n=160, bs=16, H=8, D=128), id="bf16-3groups"),
+    pytest.param(torch.float16, dict(L=2, pool=2048, n=1200, bs=16, H=2, D=64), id="fp16-cpt1"),
+]
+
+
+@pytest.mark.parametrize("dtype,geom", COOP_CASES)
+def test_fp8_tensor_single_read_bitexact(dtype, geom):
+    values, src_ids, dst_ids = _codec_case(dtype, 12, geom)
+    # an out-of-range block id: that page is skipped (its codes stay as they
+    # were, zero here) and flagged; the others' scale ignores it
+    src_ids = src_ids.clone()
+    bad = 7
+    src_ids[bad] = geom["pool"] + 3
+    L, n, bs, H, D = geom["L"], geom["n"], geom["bs"], geom["H"], geom["D"]
+    cache = _cache_from(values)
+    view = _paged.cache_view(cache)
+    layout = _paged.BlobLayout("fp8_e4m3", 2, n, bs, H, D)
+    blobs = [torch.zeros(layout.total_bytes, dtype=torch.uint8, device=DEV) for _ in range(L)]
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _paged.quant_gather(layout, view, src_ids, [b.data_ptr() for b in blobs], 2, err_flag=flag)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == amf_hip.ERRFLAG_BLOCK_RANGE
+    ok_ids = src_ids.clone()
+    ok_ids[bad] = 0
+    for l, blob in enumerate(blobs):
+        pages = _pages(values, l, ok_ids).clone()
+        pages[:, bad] = 0
+        codes, scale = oc.fp8_tensor_compress(pages)
+        assert np.array_equal(bytes_of(_seg(blob, 0, layout.data_bytes)), bytes_of(codes)), l
+        side = _seg(blob, layout.scale_offset, 16).view(torch.float32).cpu()
+        assert torch.equal(side, oc.fp8_sidecar(scale)), l
+
+
 @pytest.mark.parametrize("dtype,geom", CODEC_CASES)
 def test_fp8_page_head_format_bitexact(dtype, geom):
     values, src_ids, dst_ids = _codec_case(dtype, 20, geom)
