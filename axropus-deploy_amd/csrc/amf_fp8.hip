@@ -69,9 +69,12 @@ template <int DT, bool PER_TENSOR>
 __global__ __launch_bounds__(kThreads) void fp8_dequant_scatter_kernel(
     const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
-    const int32_t* __restrict__ block_ids, int64_t pool, PageGeom g, int32_t* err_flag) {
-  const int64_t j = blockIdx.x;
-  const int plane = blockIdx.y;
+    const int32_t* __restrict__ block_ids, int64_t pool, int64_t n_pages, int n_planes,
+    PageGeom g, int32_t* err_flag) {
+  const PageWork pw = xcd_page_work(n_pages, n_planes);
+  if (!pw.valid) return;
+  const int64_t j = pw.j;
+  const int plane = pw.plane;
   const int64_t dp = block_ids ? (int64_t)block_ids[j] : j;
   if (dp < 0 || dp >= pool) {
     if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
@@ -822,13 +825,16 @@ extern "C" int amf_fp8_dequant_scatter(int32_t format, const uint64_t* code_plan
   PageGeom g;
   if ((rc = make_geom(who, block_size, num_heads, head_dim, 1, &g))) return rc;
   if (n_pages == 0) return ok();
-  dim3 grid((unsigned)n_pages, (unsigned)n_planes);
+  if (n_pages * n_planes > 0x7FFFFFF0ll)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: %lld pages x %d planes exceed one launch", who,
+                (long long)n_pages, n_planes);
+  const dim3 grid = xcd_page_grid(n_pages, n_planes);
   hipStream_t s = as_stream(stream);
   const bool pt = format == AMF_FMT_FP8_E4M3;
-#define AMF_LAUNCH(T)                                                                      \
-  fp8_dequant_scatter_kernel<DT, T><<<grid, kThreads, 0, s>>>(                             \
-      code_planes, param_planes, cache_planes, cache_page_stride, block_ids, pool_pages, g, \
-      err_flag)
+#define AMF_LAUNCH(T)                                                                       \
+  fp8_dequant_scatter_kernel<DT, T><<<grid, kThreads, kRestoreLdsPad, s>>>(                 \
+      code_planes, param_planes, cache_planes, cache_page_stride, block_ids, pool_pages,     \
+      n_pages, n_planes, g, err_flag)
   AMF_WITH_DTYPE(cache_dtype, if (pt) AMF_LAUNCH(true); else AMF_LAUNCH(false));
 #undef AMF_LAUNCH
   return check_launch(who);

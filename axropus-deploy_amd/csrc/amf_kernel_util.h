@@ -16,6 +16,42 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// ---- restore work mapping ------------------------------------------------------
+// The FP8 and INT4-sym restores write whole pages at block-table-chosen
+// places.  Their grid is 1-D: workgroup id runs on XCD id % 8 (round-robin
+// dispatch), and xcd_page_work gives XCD x the contiguous eighth x of the
+// plane-major (plane, page) list, so each XCD's in-flight pages come from one
+// or two planes instead of from every plane.  The FP8 restore is launched
+// with kRestoreLdsPad bytes of (unused) dynamic LDS, which holds a CU to
+// three of its workgroups: fewer pages in flight per XCD, still enough bytes
+// in flight for the HBM (the INT4 restores, which write four times what they
+// read, lose with the pad).
+constexpr unsigned kRestoreLdsPad = 52u << 10;
+
+struct PageWork {
+  int64_t j;   // position in the gathered sequence
+  int plane;
+  bool valid;  // false for the up to 7 padding workgroups
+};
+
+__host__ __device__ inline int64_t xcd_page_items_per_xcd(int64_t n_pages, int n_planes) {
+  return (n_pages * n_planes + 7) / 8;
+}
+
+__device__ __forceinline__ PageWork xcd_page_work(int64_t n_pages, int n_planes) {
+  const int64_t id = blockIdx.x;
+  const int64_t w = (id & 7) * xcd_page_items_per_xcd(n_pages, n_planes) + (id >> 3);
+  PageWork r;
+  r.valid = w < n_pages * n_planes;
+  r.plane = (int)(w / n_pages);
+  r.j = w - (int64_t)r.plane * n_pages;
+  return r;
+}
+
+inline dim3 xcd_page_grid(int64_t n_pages, int n_planes) {
+  return dim3((unsigned)(8 * xcd_page_items_per_xcd(n_pages, n_planes)));
+}
+
 // ---- streaming loads / stores -------------------------------------------------
 // Data read or written once per launch (codes, restored pages) goes through
 // these; AMF_USE_NT selects the non-temporal cache policy.
