@@ -764,6 +764,10 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
 #endif
 constexpr int64_t kTargetWaves = AMF_DECODE_TARGET_WAVES;
 constexpr int kMaxSplitTokens = 1024;  // 64 pages: one block-table entry per lane
+#ifndef AMF_DECODE_MIN_SPLIT
+#define AMF_DECODE_MIN_SPLIT 256
+#endif
+constexpr int kMinSplitTokens = AMF_DECODE_MIN_SPLIT;
 #ifndef AMF_DECODE_MAX_SPLITS
 #define AMF_DECODE_MAX_SPLITS 128
 #endif
@@ -775,7 +779,7 @@ int choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context_len
   const int64_t per_seq = ((int64_t)max_context_len + kMaxSplitsPerSeq - 1) / kMaxSplitsPerSeq;
   if (split < per_seq) split = per_seq;
   split = (split + 31) / 32 * 32;
-  if (split < 256) split = 256;
+  if (split < kMinSplitTokens) split = kMinSplitTokens;
   if (split > kMaxSplitTokens) split = kMaxSplitTokens;
   return (int)split;
 }
