@@ -195,13 +195,22 @@ def dtype_tag(dtype) -> int:
     raise ValueError(f"unsupported dtype {dtype}")
 
 
+_CUDA_READY = False
+
+
 def _device_index(device) -> int:
+    global _CUDA_READY
     import torch
 
-    if not torch.cuda.is_initialized():
-        torch.cuda.init()
+    if not _CUDA_READY:
+        if not torch.cuda.is_initialized():
+            torch.cuda.init()
+        _CUDA_READY = True
     if isinstance(device, int):
         return device
+    idx = getattr(device, "index", None)
+    if idx is not None:
+        return idx
     dev = torch.device(device)
     return torch.cuda.current_device() if dev.index is None else dev.index
 

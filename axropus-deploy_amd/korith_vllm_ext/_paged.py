@@ -204,13 +204,20 @@ def _elem_size(dtype: torch.dtype) -> int:
     return torch.empty((), dtype=dtype).element_size()
 
 
-def _kv_of(layer: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    if layer.dim() == 5 and layer.shape[0] == 2:
-        return layer[0], layer[1]
-    if layer.dim() == 4:
-        return layer, layer
+def _kv_planes(layer: torch.Tensor):
+    """(K address, V address), plane shape [num_blocks, block_size, H, D] and
+    plane strides (elements) of one layer, from its own shape and strides (no
+    per-plane tensor is built: this runs once per layer on every save/load)."""
+    shape = layer.shape
+    st = layer.stride()
+    if len(shape) == 5 and shape[0] == 2:
+        base = layer.data_ptr()
+        return (base, base + st[0] * layer.element_size()), tuple(shape[1:]), st[1:]
+    if len(shape) == 4:
+        base = layer.data_ptr()
+        return (base, base), tuple(shape), st
     raise ValueError(
-        f"KV cache layer of shape {tuple(layer.shape)}: expected [2, num_blocks, block_size, H, D]"
+        f"KV cache layer of shape {tuple(shape)}: expected [2, num_blocks, block_size, H, D]"
         " or [num_blocks, block_size, H, D]"
     )
 
@@ -221,17 +228,15 @@ def cache_view(gpu_cache: Sequence[torch.Tensor]) -> CacheView:
     planes: List[int] = []
     geom = None
     for layer in gpu_cache:
-        for t in _kv_of(layer):
-            nb, bs, H, D = t.shape
-            es = t.element_size()
-            if t.stride(3) != 1 or t.stride(2) != D or t.stride(1) != H * D:
-                raise ValueError("KV cache pages must be contiguous [block_size][H][D]")
-            g = (nb, bs, H, D, t.stride(0) * es, t.dtype, t.device)
-            if geom is None:
-                geom = g
-            elif g != geom:
-                raise ValueError(f"KV cache layers differ in geometry: {g} vs {geom}")
-            planes.append(t.data_ptr())
+        addrs, (nb, bs, H, D), st = _kv_planes(layer)
+        if st[3] != 1 or st[2] != D or st[1] != H * D:
+            raise ValueError("KV cache pages must be contiguous [block_size][H][D]")
+        g = (nb, bs, H, D, st[0] * layer.element_size(), layer.dtype, layer.device)
+        if geom is None:
+            geom = g
+        elif g != geom:
+            raise ValueError(f"KV cache layers differ in geometry: {g} vs {geom}")
+        planes.extend(addrs)
     nb, bs, H, D, stride, dtype, device = geom
     return CacheView(planes, stride, nb, bs, H, D, dtype, device, keep=list(gpu_cache))
 

@@ -31,6 +31,7 @@ There is no CPU fallback: the pool needs a HIP device and libamf_hip.so.
 
 from __future__ import annotations
 
+import collections.abc
 import logging
 import math
 import threading
@@ -104,7 +105,7 @@ class PoolEntry:
     num_tokens: int
     format: str
     blocks: List[CompressedBlock]
-    blobs: List[CompressedKV]
+    blobs: Sequence[CompressedKV]  # per layer, built on first access
 
     created_ns: int = 0
     last_hit_ns: int = 0
@@ -119,6 +120,40 @@ class PoolEntry:
 
     def nbytes(self) -> int:
         return sum(b.data_bytes + b.scale_bytes for b in self.blocks)
+
+
+class _EntryBlobs(collections.abc.Sequence):
+    """An entry's per-layer CompressedKV views of its slab spans, each built
+    on first access.  The save and restore launches work from the entry's
+    blocks and layout, so a save of L layers no longer builds L sets of
+    tensor views that only a later caller of entry.blobs reads."""
+
+    __slots__ = ("_make", "_items")
+
+    def __init__(self, n: int, make) -> None:
+        self._make = make
+        self._items: List[Optional[CompressedKV]] = [None] * n
+
+    def __len__(self) -> int:
+        return len(self._items)
+
+    def __getitem__(self, l):
+        if isinstance(l, slice):
+            return [self[i] for i in range(*l.indices(len(self._items)))]
+        n = len(self._items)
+        if not -n <= l < n:
+            raise IndexError(l)
+        l = l % n
+        blob = self._items[l]
+        if blob is None:
+            blob = self._items[l] = self._make(l)
+        return blob
+
+    def __setitem__(self, l: int, blob: CompressedKV) -> None:
+        self._items[l] = blob
+
+    def built(self, l: int) -> bool:
+        return self._items[l] is not None
 
 
 # ------------------------------------------------------------ allocator --
@@ -651,25 +686,37 @@ class CompressedVRAMPool:
                     pending = (host, ev)
             codec = None if fmt == FMT_RAW else get_codec(fmt)
             T = shape[1] * shape[2] if len(shape) == 5 else shape[1]  # tokens per plane
-            blocks, blobs = [], []
-            for l, (start, _) in enumerate(spans):
-                off = start * self.block_bytes
+            # tensor_scale: 1.0 for every format but per-tensor FP8, whose
+            # scale arrives with pending_absmax (0.0 until then)
+            scale0 = 0.0 if pending is not None else 1.0
+            blocks = [CompressedBlock(
+                layer_id=l, block_id=start, format=fmt, num_tokens=n_tokens,
+                num_heads=layout.num_heads, head_dim=layout.head_dim,
+                data_offset=start * self.block_bytes, data_bytes=layout.data_bytes,
+                scale_offset=start * self.block_bytes + layout.scale_offset,
+                scale_bytes=layout.scale_bytes, tensor_scale=scale0,
+                meta={"_layout": layout, "n_tokens": T}, span_blocks=need)
+                for l, (start, _) in enumerate(spans)]
+            slabs = self._slabs
+
+            def make_blob(l: int) -> CompressedKV:
+                # Reads the block's current offset (compaction moves spans)
+                # and scale; the blob shares the block's meta dict.
+                blk = blocks[l]
                 if codec is None:
-                    data = self._slabs[l].narrow(0, off, layout.data_bytes).view(dtype)
-                    blob = CompressedKV(format=FMT_RAW, data=data.view(shape), scales=None,
+                    data = slabs[l].narrow(0, blk.data_offset, layout.data_bytes).view(dtype)
+                    return CompressedKV(format=FMT_RAW, data=data.view(shape), scales=None,
                                         tensor_scale=1.0, shape=shape, dtype_original=dtype,
-                                        meta={"_layout": layout, "n_tokens": T})
-                else:
-                    # per-tensor FP8: the scale arrives with pending_absmax
-                    blob = codec.wrap_blob(self._slabs[l], off, layout, shape, dtype, None, T,
-                                           scale=0.0 if pending is not None else None)
-                blobs.append(blob)
-                blocks.append(CompressedBlock(
-                    layer_id=l, block_id=start, format=fmt, num_tokens=n_tokens,
-                    num_heads=layout.num_heads, head_dim=layout.head_dim, data_offset=off,
-                    data_bytes=layout.data_bytes, scale_offset=off + layout.scale_offset,
-                    scale_bytes=layout.scale_bytes, tensor_scale=blob.tensor_scale,
-                    meta=blob.meta, span_blocks=need))
+                                        meta=blk.meta)
+                blob = codec.wrap_blob(slabs[l], blk.data_offset, layout, shape, dtype, None, T,
+                                       scale=blk.tensor_scale if fmt == FMT_FP8_E4M3 else None)
+                blk.meta.update(blob.meta)
+                blob.meta = blk.meta
+                return blob
+
+            # (per-tensor FP8 entries always carry pending_absmax here, so
+            # blk.tensor_scale is 0.0 until resolved, then the scale)
+            blobs = _EntryBlobs(L, make_blob)
             now = time.monotonic_ns()
             entry = PoolEntry(prefix_hash=prefix_hash, num_layers=L, num_tokens=n_tokens,
                               format=fmt, blocks=blocks, blobs=blobs, created_ns=now,
@@ -689,11 +736,14 @@ class CompressedVRAMPool:
         host, ev = entry.pending_absmax
         ev.synchronize()
         vals = host.view(torch.float32).tolist()
-        for l, (blk, blob) in enumerate(zip(entry.blocks, entry.blobs)):
+        blobs = entry.blobs
+        for l, blk in enumerate(entry.blocks):
             scale = tensor_scale_from_absmax(vals[l], entry.cache_dtype)
             blk.tensor_scale = scale
-            blob.tensor_scale = scale
-            blob.meta["sidecar"] = FP8ScaleSidecar(k_scale=scale, v_scale=scale)
+            # blk.meta is the blob's meta once the blob exists
+            blk.meta["sidecar"] = FP8ScaleSidecar(k_scale=scale, v_scale=scale)
+            if not isinstance(blobs, _EntryBlobs) or blobs.built(l):
+                blobs[l].tensor_scale = scale
         entry.pending_absmax = None
 
     def _fence(self, entry: PoolEntry) -> None:
@@ -794,6 +844,8 @@ class CompressedVRAMPool:
                 entry.fences = {int(stream.cuda_stream): ev}
 
     def _rewrap(self, entry: PoolEntry, blk: CompressedBlock) -> None:
+        if isinstance(entry.blobs, _EntryBlobs) and not entry.blobs.built(blk.layer_id):
+            return  # built later from the block's new offset
         old = entry.blobs[blk.layer_id]
         if entry.format == FMT_RAW:
             data = self._slabs[blk.layer_id].narrow(0, blk.data_offset, blk.data_bytes)
