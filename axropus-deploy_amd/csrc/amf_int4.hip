@@ -47,6 +47,11 @@ __device__ __forceinline__ void load32(const uint8_t* p, float* x) {
   for (int q = 0; q < 4; ++q) load8<DT>(p + q * (8 * elem_bytes<DT>()), x + 8 * q);
 }
 
+// Code words a sym-restore lane keeps in flight before its stores.
+#ifndef AMF_SYM_RESTORE_UNROLL
+#define AMF_SYM_RESTORE_UNROLL AMF_RESTORE_UNROLL
+#endif
+
 // CHANNEL = false: INT4_SYM_BLOCK (params: [n_pages] fp16);
 // CHANNEL = true : INT4_SYM       (params: [head_dim] fp16 per scale group).
 // One lane = one 8-element chunk (4 code bytes in, one 16-byte vector out):
@@ -82,7 +87,7 @@ __global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
 #pragma unroll
     for (int q = 0; q < 8; ++q) s_ch[q] = (float)params[d0 + q];
   }
-  constexpr int U = AMF_RESTORE_UNROLL;
+  constexpr int U = AMF_SYM_RESTORE_UNROLL;
   for (int base = tid; base < n8; base += U * kThreads) {
     uint32_t c[U];
 #pragma unroll

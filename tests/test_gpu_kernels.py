@@ -199,6 +199,41 @@ def test_fp8_tensor_single_read_bitexact(dtype, geom):
         assert torch.equal(side, oc.fp8_sidecar(scale)), l
 
 
+def test_fp8_tensor_single_read_beside_another_stream():
+    """The cooperative per-tensor save issued while restores run on a second
+    stream (default priority): it completes without a sync give-up and its
+    codes still equal the oracle's."""
+    dtype, geom = torch.bfloat16, dict(L=3, pool=512, n=160, bs=16, H=8, D=128)
+    values, src_ids, dst_ids = _codec_case(dtype, 14, geom)
+    L, n, bs, H, D = geom["L"], geom["n"], geom["bs"], geom["H"], geom["D"]
+    cache = _cache_from(values)
+    view = _paged.cache_view(cache)
+    layout = _paged.BlobLayout("fp8_e4m3", 2, n, bs, H, D)
+    blobs = [torch.zeros(layout.total_bytes, dtype=torch.uint8, device=DEV) for _ in range(L)]
+    # busy work for the side stream: restores of a PH blob into a scratch cache
+    ph = _paged.BlobLayout("fp8_e4m3_ph", 2, n, bs, H, D)
+    ph_blobs = [torch.zeros(ph.total_bytes, dtype=torch.uint8, device=DEV) for _ in range(L)]
+    _paged.quant_gather(ph, view, src_ids, [b.data_ptr() for b in ph_blobs], 2)
+    scratch = [torch.empty_like(c) for c in cache]
+    sview = _paged.cache_view(scratch)
+    torch.cuda.synchronize()
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        for _ in range(200):
+            _paged.dequant_scatter(ph, [b.data_ptr() for b in ph_blobs], 2, sview, dst_ids)
+    for _ in range(3):
+        _paged.quant_gather(layout, view, src_ids, [b.data_ptr() for b in blobs], 2,
+                            err_flag=flag)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 0
+    for l, blob in enumerate(blobs):
+        codes, scale = oc.fp8_tensor_compress(_pages(values, l, src_ids))
+        assert np.array_equal(bytes_of(_seg(blob, 0, layout.data_bytes)), bytes_of(codes)), l
+        side_scale = _seg(blob, layout.scale_offset, 16).view(torch.float32).cpu()
+        assert torch.equal(side_scale, oc.fp8_sidecar(scale)), l
+
+
 @pytest.mark.parametrize("dtype,geom", CODEC_CASES)
 def test_fp8_page_head_format_bitexact(dtype, geom):
     values, src_ids, dst_ids = _codec_case(dtype, 20, geom)
