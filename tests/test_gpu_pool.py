@@ -256,6 +256,39 @@ def test_compaction_keeps_entries_restorable():
         assert torch.equal(after, before[k])
 
 
+def test_entry_blob_views_follow_their_spans():
+    """entry.blobs are built on first access: views made before a compaction
+    are re-cut to the moved spans, views made after it start at the new
+    offsets, and every view decodes to what restore_to_tensor returns."""
+    from korith_vllm_ext.codecs import FP8ScaleSidecar, get_codec
+
+    p = _pool(num_layers=2, bytes_per_layer=1 << 20, block_bytes=1 << 13,
+              default_format="fp8_e4m3")
+    g = torch.Generator().manual_seed(6)
+    vals = {k: gen.kv_values((2, 2, 8, 16, 2, 64), 64, g, True) for k in "abc"}
+    for k, v in vals.items():
+        assert p.put_from_vllm(k, [v[l].to(DEV) for l in range(2)], list(range(8)), 128)
+    e_b = p._index["b"]
+    assert e_b.blobs[0].tensor_scale == 0.0            # built before its scale resolved
+    p.delete("a")
+    p._compact_slabs()
+    codec = get_codec("fp8_e4m3")
+    for k in "bc":
+        e = p.get(k)                                    # resolves the per-tensor scales
+        want = p.restore_to_tensor(k, torch.bfloat16)
+        for l in range(2):
+            blk, blob = e.blocks[l], e.blobs[l]
+            assert blob.data.data_ptr() == p._slabs[l].data_ptr() + blk.data_offset
+            assert blob.tensor_scale == blk.tensor_scale > 0
+            assert isinstance(blob.meta["sidecar"], FP8ScaleSidecar)
+            assert blob.meta is blk.meta
+            assert torch.equal(codec.decompress_to(blob, torch.bfloat16), want[l])
+    assert len(e.blobs) == 2 and e.blobs[-1] is e.blobs[1]
+    assert [b.data.data_ptr() for b in e.blobs[0:2]] == [b.data.data_ptr() for b in e.blobs]
+    with pytest.raises(IndexError):
+        e.blobs[2]
+
+
 # ------------------------------------------------------------- AMFK files --
 
 
