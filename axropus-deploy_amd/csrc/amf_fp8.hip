@@ -11,10 +11,7 @@
 // 16-element column chunk (tid % (head_dim/16)) of rows tid / (head_dim/16),
 // + rows_per_iter, ...  Code chunks are 16-byte loads/stores, cache chunks two
 // 16-byte vectors.
-#include <map>
-#include <mutex>
-#include <utility>
-
+#include "amf_coop.h"
 #include "amf_internal.h"
 #include "amf_kernel_util.h"
 
@@ -236,101 +233,25 @@ __global__ void fp8_tensor_finalize_kernel(const uint64_t* __restrict__ param_pl
 // of each page (tid + 256 m), so page addresses are workgroup-uniform.  The
 // host takes this path only when a group fits the grid; others take the
 // two-pass kernels.
-constexpr int kCoopChunks = 16;
-constexpr int kCoopThreads = 256;
-constexpr uint32_t kCoopSpinLimit = 1u << 20;
-constexpr int kCoopClusters = kFp8CoopClusters;
-constexpr int kLineWords = kFp8CoopLineWords;  // one 128-byte line
-constexpr uint32_t kReady = 0x80000000u;  // above every non-negative float's bits
-
 struct CoopArgs {
-  const uint64_t* cache_planes;
-  int64_t cache_stride;
-  const int32_t* block_ids;
-  int64_t pool;
+  CoopGeom geo;
   const uint64_t* code_planes;
-  int64_t n_pages;
-  int64_t group_pages;  // pps * n_pages
   int64_t page_elems;
-  int pps;
-  int n_groups;
-  int ppw;              // pages per workgroup per group
   uint32_t* ws;         // [n_groups] absmax bits, written by each group's root
   // Per group, kCoopClusters + 1 lines, zeroed before the launch.  Cluster
   // line k: [0] arrivals, [1] max bits, [2] the group's max | kReady once
   // complete.  Root line: [0] clusters complete, [1] max bits.
   uint32_t* sync;
-  int32_t* err_flag;
 };
 
-__device__ __forceinline__ uint32_t* coop_line(const CoopArgs& a, int gi, int k) {
-  return a.sync + ((int64_t)gi * (kCoopClusters + 1) + k) * kLineWords;
-}
-
-// Page i of this workgroup in group gi: its plane and gathered position,
-// whether it exists, and whether it also has an in-range block id (sp).
-struct CoopPage {
-  bool exists;
-  bool ok;
-  int plane;
-  int64_t j;
-  int64_t sp;
-};
-
-__device__ __forceinline__ CoopPage coop_page(const CoopArgs& a, int gi, int i) {
-  CoopPage r;
-  const int64_t pg = blockIdx.x + (int64_t)i * gridDim.x;
-  r.exists = i < a.ppw && pg < a.group_pages;
-  r.ok = r.exists;
-  r.plane = 0;
-  r.j = 0;
-  r.sp = -1;
-  if (r.exists) {
-    const int pl = (int)(pg / a.n_pages);
-    r.plane = gi * a.pps + pl;
-    r.j = pg - (int64_t)pl * a.n_pages;
-    r.sp = a.block_ids ? (int64_t)a.block_ids[r.j] : r.j;
-    r.ok = r.sp >= 0 && r.sp < a.pool;
-  }
-  return r;
-}
-
-// Loads the workgroup's pages of group gi; absent pages and pages whose
-// block id is out of range read as zero (and are never stored).
-template <int CPT>
-__device__ __forceinline__ void coop_load(const CoopArgs& a, int gi, u32x4 (&buf)[kCoopChunks]) {
-#pragma unroll
-  for (int i = 0; i < kCoopChunks / CPT; ++i) {
-    const CoopPage q = coop_page(a, gi, i);
-    if (q.ok) {
-      const u32x4* src = reinterpret_cast<const u32x4*>(
-          reinterpret_cast<const uint8_t*>(a.cache_planes[q.plane]) + q.sp * a.cache_stride);
-#pragma unroll
-      for (int m = 0; m < CPT; ++m)
-        buf[i * CPT + m] = ld_stream(src + threadIdx.x + kCoopThreads * m);
-    } else {
-#pragma unroll
-      for (int m = 0; m < CPT; ++m) buf[i * CPT + m] = u32x4{0u, 0u, 0u, 0u};
-      if (q.exists && threadIdx.x == 0 && a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_BLOCK_RANGE);
-    }
-  }
-}
-
-// The absmax works on the 16-bit patterns: for non-NaN values |x| orders as
-// its bits with the sign cleared, and NaN patterns (above the infinity
-// pattern) are dropped, as fmaxf drops them in the two-pass kernel.  Not
-// converting to fp32 here also keeps the compiler from holding converted
-// copies of the buffer until the store.
+// The absmax works on the 16-bit patterns (abs_bits16): not converting to
+// fp32 here also keeps the compiler from holding converted copies of the
+// buffer until the store.
 template <int DT>
 __device__ __forceinline__ uint32_t absmax_bits16(const u32x4& v, uint32_t m) {
-  constexpr uint32_t kInf = DT == AMF_DTYPE_BF16 ? 0x7F80u : 0x7C00u;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    uint32_t lo = v[q] & 0x7FFFu, hi = (v[q] >> 16) & 0x7FFFu;
-    lo = lo > kInf ? 0u : lo;
-    hi = hi > kInf ? 0u : hi;
-    m = max(m, max(lo, hi));
-  }
+  for (int q = 0; q < 4; ++q)
+    m = max(m, max(abs_bits16<DT>(v[q] & 0xFFFFu), abs_bits16<DT>(v[q] >> 16)));
   return m;
 }
 
@@ -364,13 +285,13 @@ __device__ __forceinline__ void coop_arrive(const CoopArgs& a, int gi,
     const int k = (int)blockIdx.x % kCoopClusters;
     const int n_clusters = G < kCoopClusters ? G : kCoopClusters;
     const uint32_t members = (uint32_t)((G - k + kCoopClusters - 1) / kCoopClusters);
-    uint32_t* cl = coop_line(a, gi, k);
+    uint32_t* cl = coop_line(a.sync, gi, k);
     __hip_atomic_fetch_max(cl + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);  // the max has completed before the count moves
     if (__hip_atomic_fetch_add(cl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
         members - 1) {
       const uint32_t cm = __hip_atomic_load(cl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      uint32_t* root = coop_line(a, gi, kCoopClusters);
+      uint32_t* root = coop_line(a.sync, gi, kCoopClusters);
       __hip_atomic_fetch_max(root + 1, cm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __builtin_amdgcn_s_waitcnt(0);
       if (__hip_atomic_fetch_add(root, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -379,7 +300,7 @@ __device__ __forceinline__ void coop_arrive(const CoopArgs& a, int gi,
             __hip_atomic_load(root + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_fetch_max(a.ws + gi, gm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (int c = 0; c < n_clusters; ++c)
-          __hip_atomic_store(coop_line(a, gi, c) + 2, gm | kReady, __ATOMIC_RELAXED,
+          __hip_atomic_store(coop_line(a.sync, gi, c) + 2, gm | kReady, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
       }
     }
@@ -397,12 +318,12 @@ __device__ __forceinline__ void coop_arrive(const CoopArgs& a, int gi,
 __device__ __forceinline__ uint32_t coop_wait(const CoopArgs& a, int gi, uint32_t* s_bits,
                                               bool& gave_up) {
   if (threadIdx.x == 0) {
-    const uint32_t* go = coop_line(a, gi, (int)blockIdx.x % kCoopClusters) + 2;
+    const uint32_t* go = coop_line(a.sync, gi, (int)blockIdx.x % kCoopClusters) + 2;
     uint32_t v = __hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t spins = 0;
     while (!gave_up && !(v & kReady)) {
       if (++spins > kCoopSpinLimit) {
-        if (a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_SYNC);
+        if (a.geo.err_flag) atomicOr(a.geo.err_flag, AMF_ERRFLAG_SYNC);
         gave_up = true;
       }
       __builtin_amdgcn_s_sleep(2);
@@ -426,7 +347,7 @@ __device__ __forceinline__ void coop_store(const CoopArgs& a, int gi,
   const float trcp = 1.0f / tdiv;
 #pragma unroll
   for (int i = 0; i < kCoopChunks / CPT; ++i) {
-    const CoopPage q = coop_page(a, gi, i);
+    const CoopPage q = coop_page(a.geo, gi, i);
     if (!q.ok) continue;
     u32x2* codes = reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(a.code_planes[q.plane]) +
                                             q.j * a.page_elems);
@@ -451,10 +372,10 @@ __global__ __launch_bounds__(kCoopThreads) void fp8_tensor_coop_kernel(CoopArgs 
   __shared__ uint32_t s_bits;
   bool gave_up = false;  // lane 0's: a wait ran out of its bound
   u32x4 b0[kCoopChunks], b1[kCoopChunks];
-  const int ng = a.n_groups;
-  coop_load<CPT>(a, 0, b0);
+  const int ng = a.geo.n_groups;
+  coop_load<CPT>(a.geo, 0, b0);
   coop_arrive<DT>(a, 0, b0, s_max);
-  if (ng > 1) coop_load<CPT>(a, 1, b1);
+  if (ng > 1) coop_load<CPT>(a.geo, 1, b1);
   // Groups in pairs so that each buffer is a fixed register array.  A group
   // is reported as soon as the previous group's max is known (its loads were
   // issued before that wait), ahead of the previous group's stores, so the
@@ -464,12 +385,12 @@ __global__ __launch_bounds__(kCoopThreads) void fp8_tensor_coop_kernel(CoopArgs 
     const uint32_t m0 = coop_wait(a, gi, &s_bits, gave_up);
     if (gi + 1 < ng) coop_arrive<DT>(a, gi + 1, b1, s_max);
     coop_store<DT, CPT>(a, gi, b0, m0);
-    if (gi + 2 < ng) coop_load<CPT>(a, gi + 2, b0);
+    if (gi + 2 < ng) coop_load<CPT>(a.geo, gi + 2, b0);
     if (gi + 1 >= ng) break;
     const uint32_t m1 = coop_wait(a, gi + 1, &s_bits, gave_up);
     if (gi + 2 < ng) coop_arrive<DT>(a, gi + 2, b0, s_max);
     coop_store<DT, CPT>(a, gi + 1, b1, m1);
-    if (gi + 3 < ng) coop_load<CPT>(a, gi + 3, b1);
+    if (gi + 3 < ng) coop_load<CPT>(a.geo, gi + 3, b1);
   }
 }
 
@@ -731,30 +652,6 @@ const void* coop_kernel(int dt, int cpt) {
 #undef AMF_COOP
 }
 
-// Workgroups of a cooperative kernel that the current device keeps resident
-// at once (0: no cooperative launch).  Queried once per (device, kernel).
-int coop_blocks(const void* fn) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  static std::mutex mu;
-  static std::map<std::pair<int, const void*>, int> cache;
-  std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_pair(dev, fn);
-  auto it = cache.find(key);
-  if (it != cache.end()) return it->second;
-  int coop = 0, cus = 0, per_cu = 0;
-  hipError_t e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kCoopThreads, 0);
-  if (e != hipSuccess) (void)hipGetLastError();
-  const int blocks = (e == hipSuccess && coop) ? per_cu * cus : 0;
-  cache[key] = blocks;
-  return blocks;
-}
-
-// Smallest scale group (bytes of cache read) worth the cooperative path: a
-// smaller group's wait costs more than its second read.
-constexpr int64_t kCoopMinGroupBytes = 4ll << 20;
 constexpr int kCoopNotTaken = 1;
 
 // Per-tensor save through fp8_tensor_coop_kernel when the device supports a
@@ -782,20 +679,20 @@ int try_tensor_coop(int32_t dt, const uint64_t* cache_planes, int64_t cache_page
   const int64_t ppw = (group_pages + blocks - 1) / blocks;
   if (ppw > kCoopChunks / cpt) return kCoopNotTaken;
   CoopArgs a;
-  a.cache_planes = cache_planes;
-  a.cache_stride = cache_page_stride;
-  a.block_ids = block_ids;
-  a.pool = pool_pages;
+  a.geo.cache_planes = cache_planes;
+  a.geo.cache_stride = cache_page_stride;
+  a.geo.block_ids = block_ids;
+  a.geo.pool = pool_pages;
+  a.geo.n_pages = n_pages;
+  a.geo.group_pages = group_pages;
+  a.geo.pps = g.pps;
+  a.geo.n_groups = n_groups;
+  a.geo.ppw = (int)ppw;
+  a.geo.err_flag = err_flag;
   a.code_planes = code_planes;
-  a.n_pages = n_pages;
-  a.group_pages = group_pages;
   a.page_elems = page_elems;
-  a.pps = g.pps;
-  a.n_groups = n_groups;
-  a.ppw = (int)ppw;
   a.ws = ws;
   a.sync = ws + fp8_tensor_sync_offset(n_groups);
-  a.err_flag = err_flag;
   void* args[] = {&a};
   const hipError_t e =
       hipLaunchCooperativeKernel(fn, dim3((unsigned)blocks), dim3(kCoopThreads), args, 0, s);

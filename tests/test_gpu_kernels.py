@@ -332,6 +332,47 @@ def test_int4_sym_channel_format_bitexact(dtype, geom):
     _check_restored(target, dst_ids, want, dtype, geom)
 
 
+# Per-channel INT4 on larger scale groups (the reduction spans several
+# absmax workgroups per plane), head_dim 128, 64 and 256, with an
+# out-of-range block id.
+CHAN_LARGE_CASES = [
+    pytest.param(torch.bfloat16, dict(L=3, pool=512, n=160, bs=16, H=8, D=128), id="bf16-d128"),
+    pytest.param(torch.float16, dict(L=2, pool=2048, n=1200, bs=16, H=2, D=64), id="fp16-d64"),
+    pytest.param(torch.bfloat16, dict(L=2, pool=256, n=160, bs=16, H=4, D=256), id="bf16-d256"),
+]
+
+
+@pytest.mark.parametrize("dtype,geom", CHAN_LARGE_CASES)
+def test_int4_sym_channel_large_groups_bitexact(dtype, geom):
+    values, src_ids, dst_ids = _codec_case(dtype, 42, geom)
+    src_ids = src_ids.clone()
+    bad = 5
+    src_ids[bad] = geom["pool"] + 1                 # skipped and flagged
+    L, n, bs, H, D = geom["L"], geom["n"], geom["bs"], geom["H"], geom["D"]
+    cache = _cache_from(values)
+    view = _paged.cache_view(cache)
+    layout = _paged.BlobLayout("int4_sym", 2, n, bs, H, D)
+    blobs = [torch.zeros(layout.total_bytes, dtype=torch.uint8, device=DEV) for _ in range(L)]
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _paged.quant_gather(layout, view, src_ids, [b.data_ptr() for b in blobs], 2, err_flag=flag)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == amf_hip.ERRFLAG_BLOCK_RANGE
+    ok_ids = src_ids.clone()
+    ok_ids[bad] = 0
+    page_bytes = bs * H * D // 2
+    for l, blob in enumerate(blobs):
+        pages = _pages(values, l, ok_ids).clone()
+        pages[:, bad] = 0                           # a skipped page adds nothing to the max
+        packed, scales = oc.int4_channel_compress(pages)
+        got = bytes_of(_seg(blob, 0, layout.data_bytes)).reshape(2, n, page_bytes)
+        want = bytes_of(packed).reshape(2, n, page_bytes)
+        keep = np.arange(n) != bad                  # the skipped page's codes stay zero
+        assert np.array_equal(got[:, keep], want[:, keep]), l
+        assert not got[:, bad].any(), l
+        sc = _seg(blob, layout.scale_offset, layout.shared_param_bytes).view(torch.float16)
+        assert torch.equal(sc.cpu(), scales), l
+
+
 @pytest.mark.parametrize("dtype,geom", CODEC_CASES)
 def test_int4_asym_g32_format_bitexact(dtype, geom):
     values, src_ids, dst_ids = _codec_case(dtype, 50, geom)
