@@ -15,6 +15,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include <map>
 #include <mutex>
@@ -27,7 +28,7 @@ namespace amf {
 
 constexpr int kCoopChunks = 16;   // 16-byte chunks per lane per register buffer
 constexpr int kCoopThreads = 256;
-constexpr uint32_t kCoopSpinLimit = 1u << 20;
+constexpr uint32_t kCoopSpinLimit = 1u << 20;  // polls before a wait gives up
 constexpr int kCoopClusters = kFp8CoopClusters;
 constexpr int kLineWords = kFp8CoopLineWords;
 constexpr uint32_t kReady = 0x80000000u;  // above every non-negative float's bits
@@ -42,8 +43,20 @@ struct CoopGeom {
   int pps;
   int n_groups;
   int ppw;              // pages per workgroup per group
+  uint32_t spin_limit;  // polls before a wait gives up (coop_spin_limit())
   int32_t* err_flag;
 };
+
+// kCoopSpinLimit, or AMF_COOP_SPIN_LIMIT from the environment (read once):
+// the tests set it to 0 to drive every wait down its give-up path, which
+// must leave the kernel to finish normally with its group scales poisoned.
+inline uint32_t coop_spin_limit() {
+  static const uint32_t limit = [] {
+    const char* e = getenv("AMF_COOP_SPIN_LIMIT");
+    return e ? (uint32_t)strtoul(e, nullptr, 10) : kCoopSpinLimit;
+  }();
+  return limit;
+}
 
 __device__ __forceinline__ uint32_t* coop_line(uint32_t* sync, int gi, int k) {
   return sync + ((int64_t)gi * (kCoopClusters + 1) + k) * kLineWords;

@@ -322,7 +322,7 @@ __device__ __forceinline__ uint32_t coop_wait(const CoopArgs& a, int gi, uint32_
     uint32_t v = __hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t spins = 0;
     while (!gave_up && !(v & kReady)) {
-      if (++spins > kCoopSpinLimit) {
+      if (++spins > a.geo.spin_limit) {
         if (a.geo.err_flag) atomicOr(a.geo.err_flag, AMF_ERRFLAG_SYNC);
         gave_up = true;
       }
@@ -688,6 +688,7 @@ int try_tensor_coop(int32_t dt, const uint64_t* cache_planes, int64_t cache_page
   a.geo.pps = g.pps;
   a.geo.n_groups = n_groups;
   a.geo.ppw = (int)ppw;
+  a.geo.spin_limit = coop_spin_limit();
   a.geo.err_flag = err_flag;
   a.code_planes = code_planes;
   a.page_elems = page_elems;

@@ -234,6 +234,59 @@ def test_fp8_tensor_single_read_beside_another_stream():
         assert torch.equal(side_scale, oc.fp8_sidecar(scale)), l
 
 
+_GIVE_UP_SCRIPT = r"""
+import sys, torch
+sys.path[:0] = sys.argv[2:4]
+from korith_vllm_ext import _paged
+cache = torch.load(sys.argv[1] + "/cache.pt", weights_only=True)
+ids = torch.load(sys.argv[1] + "/ids.pt", weights_only=True)
+L, n = len(cache), ids.numel()
+layout = _paged.BlobLayout("fp8_e4m3", 2, n, 16, 8, 128)
+blobs = [torch.zeros(layout.total_bytes, dtype=torch.uint8, device="cuda") for _ in range(L)]
+flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+view = _paged.cache_view([c.cuda() for c in cache])
+_paged.quant_gather(layout, view, ids, [b.data_ptr() for b in blobs], 2, err_flag=flag)
+torch.cuda.synchronize()
+torch.save({"flag": flag.cpu(), "blobs": [b.cpu() for b in blobs]}, sys.argv[1] + "/out.pt")
+"""
+
+
+def test_fp8_tensor_single_read_give_up_path(tmp_path):
+    """With the wait bound forced to zero polls (AMF_COOP_SPIN_LIMIT=0, read
+    once per process, hence a child process) a workgroup that finds its
+    group not yet complete takes the give-up path at once.  Whether any does
+    depends on timing (a workgroup's loads of the next group usually outlast
+    the exchange), so the check is the invariant: the launch finishes, and
+    each layer holds either the oracle's codes or an infinite scale (never
+    plausible wrong values), with AMF_ERRFLAG_SYNC raised exactly when some
+    layer is poisoned."""
+    import os
+    import subprocess
+    import sys
+
+    geom = dict(L=3, pool=512, n=160, bs=16, H=8, D=128)
+    values, src_ids, _ = _codec_case(torch.bfloat16, 16, geom)
+    torch.save([values[l].contiguous() for l in range(geom["L"])], tmp_path / "cache.pt")
+    torch.save(src_ids, tmp_path / "ids.pt")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, AMF_COOP_SPIN_LIMIT="0")
+    subprocess.run([sys.executable, "-c", _GIVE_UP_SCRIPT, str(tmp_path), root,
+                    os.path.join(root, "axropus-deploy_amd")], env=env, check=True, timeout=90)
+    out = torch.load(tmp_path / "out.pt", weights_only=True)
+    gave_up = bool(int(out["flag"].item()) & amf_hip.ERRFLAG_SYNC)
+    layout = _paged.BlobLayout("fp8_e4m3", 2, geom["n"], 16, 8, 128)
+    poisoned = 0
+    for l, blob in enumerate(out["blobs"]):
+        side = blob[layout.scale_offset:layout.scale_offset + 16].view(torch.float32)
+        if torch.isinf(side[0]):
+            poisoned += 1
+            continue
+        codes, scale = oc.fp8_tensor_compress(_pages(values, l, src_ids))
+        assert np.array_equal(bytes_of(blob[:layout.data_bytes]), bytes_of(codes)), l
+        assert torch.equal(side, oc.fp8_sidecar(scale)), l
+    assert gave_up == (poisoned > 0), (gave_up, poisoned)
+
+
 @pytest.mark.parametrize("dtype,geom", CODEC_CASES)
 def test_fp8_page_head_format_bitexact(dtype, geom):
     values, src_ids, dst_ids = _codec_case(dtype, 20, geom)
