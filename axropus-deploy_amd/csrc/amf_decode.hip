@@ -49,25 +49,11 @@ constexpr int kD = 128;          // head_dim
 constexpr int kBS = 16;          // tokens per page
 constexpr int kHBCodes = 1024;   // code bytes of one (page, head) block
 constexpr int kHBParams = 64;    // param words of one (page, head) block
-// A split's partial, kPartStride floats (16-byte rows): its output normalised
-// by its own softmax sum, O / l, as D fp16 values (a convex combination of V
-// rows, so fp16 keeps 11 bits of it at half the bytes of fp32), then m and l.
-constexpr int kPartM = kD / 2;
-constexpr int kPartL = kPartM + 1;
-constexpr int kPartStride = kPartM + 4;
+constexpr int kPartStride = kD + 4;  // split partial: D accumulators, m, l, 2 pad (16-byte rows)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1.0e30f;
 
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
-
-__device__ __forceinline__ u32x4 pack8_f16(const float* x) {
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    r[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2 * i]) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2 * i + 1]) << 16);
-  return r;
-}
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -502,21 +488,20 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     const float cv = __shfl(cf, 4 * hi + gsel);
     const int r = 4 * T + hi;
     if (r < R) {
-      // l_tot >= 1: the split's largest score has p = 1 at its last rescale.
-      const float inv_l = 1.0f / l_tot;
       float o[8];
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
         const f32x4 t = acc[T][b];
         const float v = gsel == 0 ? t[0] : gsel == 1 ? t[1] : gsel == 2 ? t[2] : t[3];
-        o[b] = (v + cv) * inv_l;
+        o[b] = v + cv;
       }
       float* base = a.ws + (((int64_t)s * a.num_q_heads + (int64_t)h * R + r) * a.max_splits + sp) *
                                kPartStride;
-      *reinterpret_cast<u32x4*>(base + 4 * lo) = pack8_f16(o);
+      *reinterpret_cast<float4*>(base + 8 * lo) = float4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<float4*>(base + 8 * lo + 4) = float4{o[4], o[5], o[6], o[7]};
       if (lo == 0) {
-        base[kPartM] = m_run[T];
-        base[kPartL] = l_tot;
+        base[kD] = m_run[T];
+        base[kD + 1] = l_tot;
       }
     }
   }
@@ -661,15 +646,13 @@ __global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
     }
     const float mr = __shfl(m_run, 16 * r), lr = __shfl(l_tot, 16 * r);
     if (hi == 0) {
-      const float inv_l = 1.0f / lr;  // >= 1, as in the MFMA kernel
-#pragma unroll
-      for (int k = 0; k < 8; ++k) o[k] *= inv_l;
       float* base = a.ws + (((int64_t)s * a.num_q_heads + (int64_t)h * R + r) * a.max_splits + sp) *
                                kPartStride;
-      *reinterpret_cast<u32x4*>(base + 4 * lo) = pack8_f16(o);
+      *reinterpret_cast<float4*>(base + 8 * lo) = float4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<float4*>(base + 8 * lo + 4) = float4{o[4], o[5], o[6], o[7]};
       if (lo == 0) {
-        base[kPartM] = mr;
-        base[kPartL] = lr;
+        base[kD] = mr;
+        base[kD + 1] = lr;
       }
     }
   }
@@ -678,8 +661,7 @@ __global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
 // ================================================================ merge ====
 
 // One workgroup of four waves per (query head, sequence):
-// O = sum_i w_i (O_i / l_i) / L with w_i = 2^(m_i - M) l_i and L = sum_i w_i,
-// written as OUT_DTYPE (an AMF_DTYPE_* tag).
+// O = sum_i 2^(m_i - M) acc_i / L, written as OUT_DTYPE (an AMF_DTYPE_* tag).
 // Split statistics are read one split per thread and the weights shared
 // through LDS; wave w sums the accumulators of splits w, w+4, ... (two dims per
 // lane, several splits in flight), and the four wave sums meet in LDS.
@@ -697,8 +679,7 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
   const int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
   const float* base = a.ws + ((int64_t)s * a.num_q_heads + qhd) * a.max_splits * kPartStride;
   float M = kNegBig;
-  for (int i = tid; i < n_sp; i += kMergeThreads)
-    M = fmaxf(M, base[(int64_t)i * kPartStride + kPartM]);
+  for (int i = tid; i < n_sp; i += kMergeThreads) M = fmaxf(M, base[(int64_t)i * kPartStride + kD]);
   M = wave_max_xor(M, 64);
   if (lane == 0) sred[w] = M;
   __syncthreads();
@@ -712,8 +693,8 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
     float wi = 0.0f;
     if (i < n_sp) {
       const float* p = base + (int64_t)i * kPartStride;
-      wi = exp2_fast(p[kPartM] - M) * p[kPartL];
-      L += wi;
+      wi = exp2_fast(p[kD] - M);
+      L += wi * p[kD + 1];
     }
     wgt[tid] = wi;
     __syncthreads();
@@ -721,10 +702,10 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
 #pragma unroll 4
     for (int k = w; k < cnt; k += kMergeWaves) {
       const float wk = wgt[k];
-      const uint32_t h2 =
-          *reinterpret_cast<const uint32_t*>(base + (int64_t)(i0 + k) * kPartStride + lane);
-      o0 += wk * (float)__builtin_bit_cast(_Float16, (uint16_t)(h2 & 0xFFFFu));
-      o1 += wk * (float)__builtin_bit_cast(_Float16, (uint16_t)(h2 >> 16));
+      const float2 v = *reinterpret_cast<const float2*>(base + (int64_t)(i0 + k) * kPartStride +
+                                                        2 * lane);
+      o0 += wk * v.x;
+      o1 += wk * v.y;
     }
   }
   for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
