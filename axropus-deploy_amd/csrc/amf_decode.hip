@@ -9,9 +9,10 @@
 // adds paging (block tables), GQA and split-K.
 //
 // Work item: one wave per (sequence, KV head, split of split_tokens tokens);
-// grid = (max_splits, num_kv_heads, num_seqs).  The wave walks its split in
-// chunks of 32 tokens (two 16-token pages) and keeps, per query head of the
-// GQA group, a running max m (log2 domain), sum l and an unnormalised output.
+// grid = (num_kv_heads, max_splits, num_seqs), or (max_splits, num_kv_heads,
+// num_seqs) past 65535 splits.  The wave walks its split in chunks of 32
+// tokens (two 16-token pages) and keeps, per query head of the GQA group, a
+// running max m (log2 domain), sum l and an unnormalised output.
 // A second kernel merges the splits.
 //
 // Dequantisation is folded into the dot products.  With K = s*c + z per
@@ -71,6 +72,7 @@ struct DecodeArgs {
   int split_tokens;
   int max_splits;
   int max_context_len;
+  int head_fast;         // grid order, see work_head
   float qk_scale_log2;  // softmax_scale * log2(e)
   float* ws;
   int32_t* err_flag;
@@ -256,6 +258,18 @@ __device__ __forceinline__ int64_t split_page(const SplitPages& sp, int pi, bool
   return v >= 0 ? (int64_t)v : 0;
 }
 
+// Work item of this wave.  With head_fast the grid is (num_kv_heads,
+// max_splits, num_seqs): the KV heads of a split are neighbouring workgroups,
+// so the codes of one page (all heads, contiguous) are read at about the same
+// time; otherwise (more splits than grid.y allows) it is (max_splits,
+// num_kv_heads, num_seqs).
+__device__ __forceinline__ int work_head(const DecodeArgs& a) {
+  return a.head_fast ? blockIdx.x : blockIdx.y;
+}
+__device__ __forceinline__ int work_split(const DecodeArgs& a) {
+  return a.head_fast ? blockIdx.y : blockIdx.x;
+}
+
 // ============================================================== MFMA path ==
 
 // One 32-token chunk of the MFMA kernel: QK^T, online softmax, PV.
@@ -387,7 +401,7 @@ template <int R, bool QBF16>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(AMF_DECODE_WAVES_PER_EU)))
 void int4_decode_mfma_kernel(DecodeArgs a) {
   constexpr int NT = (R + 3) / 4;  // 16-row tiles of (head, group) pairs
-  const int sp = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+  const int sp = work_split(a), h = work_head(a), s = blockIdx.z;
   const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
   const int ctx = clamp_context(a, s);
   const int tok_begin = sp * a.split_tokens;
@@ -512,7 +526,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
 template <int R, bool QBF16>
 __global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
   static_assert(R <= 4, "VALU path: at most 4 query heads per KV head");
-  const int sp = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+  const int sp = work_split(a), h = work_head(a), s = blockIdx.z;
   const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
   const int ctx = clamp_context(a, s);
   const int tok_begin = sp * a.split_tokens;
@@ -840,6 +854,7 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
   a.max_context_len = max_context_len;
   const int max_splits = (max_context_len + a.split_tokens - 1) / a.split_tokens;
   a.max_splits = max_splits > 0 ? max_splits : 1;
+  a.head_fast = max_splits <= 65535;
   const float scale = softmax_scale > 0.0f ? softmax_scale : 1.0f / sqrtf((float)head_dim);
   a.qk_scale_log2 = scale * kLog2e;
   a.ws = static_cast<float*>(workspace);
@@ -848,7 +863,9 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
   hipStream_t st = as_stream(stream);
   const bool bf16 = q_dtype == AMF_DTYPE_BF16;
   if (max_splits > 0) {
-    dim3 grid((unsigned)max_splits, (unsigned)num_kv_heads, (unsigned)num_seqs);
+    const dim3 grid = a.head_fast
+                          ? dim3((unsigned)num_kv_heads, (unsigned)max_splits, (unsigned)num_seqs)
+                          : dim3((unsigned)max_splits, (unsigned)num_kv_heads, (unsigned)num_seqs);
     const bool valu = algo == AMF_DECODE_VALU;
 #define AMF_LAUNCH(K, RR, B) K<RR, B><<<grid, 64, 0, st>>>(a)
 #define AMF_LAUNCH_B(K, RR) \

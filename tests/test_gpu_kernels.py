@@ -538,6 +538,24 @@ def test_int4_paged_decode_peaked_scores(algo):
     check_attention(got, ref)
 
 
+def test_int4_paged_decode_split_major_grid():
+    """More than 65535 splits (max_context_len 64M + 1 tokens at 1024-token
+    splits) selects the (max_splits, num_kv_heads, num_seqs) grid; the short
+    real contexts must decode as on the head-major grid."""
+    R, Hkv = 4, 2
+    ctxs = [1500, 37]
+    q, bt, ctx, pool, codes, params, kv32 = _decode_case(R, Hkv, ctxs, seed=91)
+    max_ctx = 65536 * 1024 + 1
+    wide = torch.full((len(ctxs), -(-max_ctx // 16)), -1, dtype=torch.int32)
+    wide[:, :bt.shape[1]] = bt
+    ref = oatt.paged_decode_f64(q.float().numpy(), kv32[0].numpy(), kv32[1].numpy(), bt.numpy(),
+                                ctx.numpy())
+    for algo in (amf_hip.DECODE_MFMA, amf_hip.DECODE_VALU):
+        got, flag = _run_decode(q, wide, ctx, pool, codes, params, Hkv, algo, max_ctx=max_ctx)
+        assert flag == 0
+        check_attention(got, ref)
+
+
 def test_int4_paged_decode_bad_page_flagged_not_faulting():
     R, Hkv = 2, 2
     q, bt, ctx, pool, codes, params, kv32 = _decode_case(R, Hkv, [64, 64], seed=90)
