@@ -143,6 +143,13 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
   return __builtin_bit_cast(uint16_t, (__bf16)x);
 }
 
+// a * b with +0 * x = +0 for every x (v_mul_legacy_f32); otherwise IEEE.
+__device__ __forceinline__ float mul_legacy(float a, float b) {
+  float r;
+  asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 __device__ __forceinline__ float pscale(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
 }
@@ -353,7 +360,6 @@ __device__ __forceinline__ void mfma_chunk(
     for (int b = 0; b < 8; ++b) vb[b] = nib8_to_bf16_128c(vw[b]);
   }
   const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
-  const bool vpage_ok = pok[vu];
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
     // A row (r', g) = (4T + lo/4, lo%4), k-slice hi: tokens 8 hi .. 8 hi + 7.
@@ -361,18 +367,17 @@ __device__ __forceinline__ void mfma_chunk(
     const float4 pa = pl[0], pb = pl[1];
     const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
     // Weights w = p * s of the lane's 8 tokens in the operand's k order, as a
-    // bf16 hi + lo pair.  A token outside the context gets a zero param word
-    // (its params may be uninitialised memory), hence w = 0 and no zero-point
-    // term.
+    // bf16 hi + lo pair.  A token outside the context or on a page with a bad
+    // id has p = +0 exactly (its score is -inf); its param words may hold any
+    // bytes, and the legacy multiply (+0 * x = +0 for every x, NaN and
+    // infinities included) keeps them out of w and of the zero-point term.
     float wk[8];
     float cs = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const bool valid = vpage_ok && (c0 + 8 * hi + e) < tok_end;
-      const uint32_t pwe = valid ? pw[e] : 0u;
-      const float sv = pscale(pwe);
-      wk[k_of_nib(e)] = pv[e] * sv;
-      cs += pv[e] * (pzero(pwe) - kCodeBias * sv);
+      const float sv = pscale(pw[e]);
+      wk[k_of_nib(e)] = mul_legacy(pv[e], sv);
+      cs += mul_legacy(pv[e], pzero(pw[e]) - kCodeBias * sv);
     }
     u32x4 ahi, alo;
 #pragma unroll
@@ -637,8 +642,10 @@ __global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
       for (int k = 0; k < 8; ++k) cv[k] = (float)__builtin_amdgcn_ubfe(vw[k], 4 * e, 4);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float pr = valid ? p_lds[vu][r][8 * vhalf + e] : 0.0f;
-        const float w = pr * sv;
+        // A token outside the context has p = 0, but its param words may hold
+        // any bytes (0 * inf = NaN): select, do not multiply, them away.
+        const float pr = p_lds[vu][r][8 * vhalf + e];
+        const float w = valid ? pr * sv : 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) accv[r][k] = __builtin_fmaf(w, cv[k], accv[r][k]);
         zacc[r] = valid ? __builtin_fmaf(pr, zv, zacc[r]) : zacc[r];

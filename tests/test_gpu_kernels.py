@@ -538,6 +538,36 @@ def test_int4_paged_decode_peaked_scores(algo):
     check_attention(got, ref)
 
 
+@pytest.mark.parametrize("algo", [amf_hip.DECODE_MFMA, amf_hip.DECODE_VALU])
+def test_int4_paged_decode_ignores_slots_past_the_context(algo):
+    """Slots past a sequence's context (the tail of its last page) may hold
+    any bytes: NaN and infinite scales and zero points there must not reach
+    the output."""
+    R, Hkv, bs = 4, 2, 16
+    ctxs = [37, 300, 1500, 7, 33]
+    q, bt, ctx, pool, codes, params, kv32 = _decode_case(R, Hkv, ctxs, seed=93)
+    u, s16, z16 = oc.int4_asym_unlayout(codes, params, bs, Hkv, 128)
+    s_bits, z_bits = s16.view(torch.int16), z16.view(torch.int16)
+    poison = [(0x7C00, 0x7E00), (0x7E00, 0xFC00 - 0x10000)]     # (+inf, NaN), (NaN, -inf)
+    n_poisoned = 0
+    for b, c in enumerate(ctxs):
+        tail = c % bs
+        if tail:
+            page = int(bt[b, c // bs])
+            for p in range(2):
+                s_bits[p, page, tail:] = poison[p][0]
+                z_bits[p, page, tail:] = poison[p][1]
+            n_poisoned += bs - tail
+    assert n_poisoned > 0
+    codes, params = oc.int4_asym_layout(u, s16, z16)
+    got, flag = _run_decode(q, bt, ctx, pool, codes, params, Hkv, algo)
+    assert flag == 0
+    ref = oatt.paged_decode_f64(q.float().numpy(), kv32[0].numpy(), kv32[1].numpy(), bt.numpy(),
+                                ctx.numpy())
+    assert np.all(np.isfinite(got))
+    check_attention(got, ref)
+
+
 def test_int4_paged_decode_split_major_grid():
     """More than 65535 splits (max_context_len 64M + 1 tokens at 1024-token
     splits) selects the (max_splits, num_kv_heads, num_seqs) grid; the short
