@@ -239,18 +239,27 @@ struct SplitPages {
   int first;  // logical page index of lane 0
 };
 
-__device__ __forceinline__ SplitPages load_split_pages(const DecodeArgs& a, const int32_t* bt,
-                                                      int tok_begin, int tok_end) {
+// Lane's raw block-table entry of split sp, read before the context length
+// is known (so the two loads overlap); bounded by the table's row only.
+__device__ __forceinline__ int split_table_entry(const DecodeArgs& a, const int32_t* bt, int sp) {
+  const int first = sp * (a.split_tokens / kBS), lane = threadIdx.x;
+  return (lane < a.split_tokens / kBS && first + lane < a.bt_stride) ? bt[first + lane] : -1;
+}
+
+// The split's pages from the raw entries: entries past the context become
+// -1 (never read); out-of-range ids inside it are reported and become -2
+// (masked, never dereferenced).
+__device__ __forceinline__ SplitPages split_pages(const DecodeArgs& a, int raw, int tok_begin,
+                                                  int tok_end) {
   SplitPages sp;
   sp.first = tok_begin / kBS;
   const int n = (tok_end - tok_begin + kBS - 1) / kBS;
-  const int lane = threadIdx.x;
   int v = -1;
-  if (lane < n) {
-    v = bt[sp.first + lane];
-    if ((v < 0 || (int64_t)v >= a.pool_pages)) {
+  if ((int)threadIdx.x < n) {
+    v = raw;
+    if (v < 0 || (int64_t)v >= a.pool_pages) {
       if (a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_BLOCK_RANGE);
-      v = -2;  // invalid id: masked, never dereferenced
+      v = -2;
     }
   }
   sp.v = v;
@@ -408,14 +417,28 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
   constexpr int NT = (R + 3) / 4;  // 16-row tiles of (head, group) pairs
   const int sp = work_split(a), h = work_head(a), s = blockIdx.z;
   const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
+  const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
+  const int bt_raw = split_table_entry(a, bt, sp);
   const int ctx = clamp_context(a, s);
   const int tok_begin = sp * a.split_tokens;
   if (tok_begin >= ctx) return;
   const int tok_end = min(ctx, tok_begin + a.split_tokens);
-  const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
   const uint16_t* qh = a.q + ((int64_t)s * a.num_q_heads + (int64_t)h * R) * kD;
 
   // ---- Q operands (constant for the wave) ----
+  // Every lane loads (rows past the GQA group clamped to its last row) and
+  // the lanes a value does not belong to zero it afterwards: loads under a
+  // lane condition would each wait for the one before.
+  u32x4 qraw[NT][5];
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    const int r = 4 * T + (lo >> 2), g = lo & 3;
+    const uint16_t* qr = qh + (r < R ? r : R - 1) * kD;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      qraw[T][st] = *reinterpret_cast<const u32x4*>(qr + 32 * hi + 8 * st);
+    qraw[T][4] = *reinterpret_cast<const u32x4*>(qr + 32 * g + 8 * hi);
+  }
   u32x4 qa_hi[NT][4], qa_lo[NT][4];
   float qsum[NT][4];
 #pragma unroll
@@ -423,26 +446,25 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     const int r = 4 * T + (lo >> 2), g = lo & 3;
     // A operand of k-step st: row (r, g) holds q[r][32 g + 8 st + e] on the
     // lanes whose k-slice (hi) is group g.
+    const bool mine = r < R && g == hi;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       // Elements in the k order of nib8_to_bf16_128c; an fp16 query is split
       // into bf16 hi + lo (a bf16 query has lo = 0).
-      u32x4 vh = {0, 0, 0, 0}, vl = {0, 0, 0, 0};
-      if (r < R && g == hi) {
-        const u32x4 raw = *reinterpret_cast<const u32x4*>(qh + r * kD + 32 * hi + 8 * st);
-        float xq[8];
+      const u32x4 raw = qraw[T][st];
+      float xq[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          xq[2 * i] = qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu));
-          xq[2 * i + 1] = qval<QBF16>((uint16_t)(raw[i] >> 16));
-        }
+      for (int i = 0; i < 4; ++i) {
+        xq[2 * i] = qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu));
+        xq[2 * i + 1] = qval<QBF16>((uint16_t)(raw[i] >> 16));
+      }
+      u32x4 vh, vl;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float x0 = xq[nib_of_k(2 * j)], x1 = xq[nib_of_k(2 * j + 1)];
-          const uint32_t hw = pack2<true>(x0, x1);
-          vh[j] = hw;
-          vl[j] = pack2<true>(x0 - u2f(hw << 16), x1 - u2f(hw & 0xFFFF0000u));
-        }
+      for (int j = 0; j < 4; ++j) {
+        const float x0 = xq[nib_of_k(2 * j)], x1 = xq[nib_of_k(2 * j + 1)];
+        const uint32_t hw = pack2<true>(x0, x1);
+        vh[j] = mine ? hw : 0u;
+        vl[j] = mine ? pack2<true>(x0 - u2f(hw << 16), x1 - u2f(hw & 0xFFFF0000u)) : 0u;
       }
       qa_hi[T][st] = vh;
       qa_lo[T][st] = vl;
@@ -451,12 +473,11 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     // them, a cross-row sum completes it, then lane (t, j) fetches the four
     // groups of head 4T + j.
     float part = 0.0f;
-    if (r < R) {
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(qh + r * kD + 32 * g + 8 * hi);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        part += qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu)) + qval<QBF16>((uint16_t)(raw[i] >> 16));
-    }
+    for (int i = 0; i < 4; ++i)
+      part += qval<QBF16>((uint16_t)(qraw[T][4][i] & 0xFFFFu)) +
+              qval<QBF16>((uint16_t)(qraw[T][4][i] >> 16));
+    part = r < R ? part : 0.0f;
     part += __shfl_xor(part, 16);
     part += __shfl_xor(part, 32);
 #pragma unroll
@@ -477,7 +498,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
 
   // Software pipeline: the next chunk's pages are in flight while the current
   // chunk computes.  The last iteration re-loads its own chunk (clamped).
-  const SplitPages spg = load_split_pages(a, bt, tok_begin, tok_end);
+  const SplitPages spg = split_pages(a, bt_raw, tok_begin, tok_end);
   const int last_c0 = tok_begin + ((tok_end - tok_begin - 1) / 32) * 32;
   bool pok_n[2];
   int64_t pg_n[2];
