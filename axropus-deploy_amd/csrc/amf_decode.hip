@@ -704,78 +704,102 @@ __global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
 
 // One workgroup of four waves per (query head, sequence):
 // O = sum_i 2^(m_i - M) acc_i / L, written as OUT_DTYPE (an AMF_DTYPE_* tag).
-// Split statistics are read one split per thread and the weights shared
-// through LDS; wave w sums the accumulators of splits w, w+4, ... (two dims per
-// lane, several splits in flight), and the four wave sums meet in LDS.
+// Thread t reads (m, l) of split t once (and of splits t + 256, ... when
+// there are more) and the weights are shared through LDS.  For the
+// accumulators, lane (half, c) of wave w reads dims 4c .. 4c + 3 of splits
+// w + 4 half, w + 4 half + 8, ...: a wave load covers two whole splits and
+// several are in flight; the halves and then the waves are summed at the end.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeWaves = kMergeThreads / 64;
 
 template <int OUT_DTYPE>
 __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(DecodeArgs a) {
   __shared__ float wgt[kMergeThreads];
-  __shared__ float red[kMergeWaves][kD];
+  __shared__ __attribute__((aligned(16))) float red[kMergeWaves][kD];
   __shared__ float sred[kMergeWaves];
   const int qhd = blockIdx.x, s = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int half = lane >> 5, c = lane & 31;
   const int ctx = clamp_context(a, s);
   const int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
   const float* base = a.ws + ((int64_t)s * a.num_q_heads + qhd) * a.max_splits * kPartStride;
-  float M = kNegBig;
-  for (int i = tid; i < n_sp; i += kMergeThreads) M = fmaxf(M, base[(int64_t)i * kPartStride + kD]);
+  float m0 = kNegBig, l0 = 0.0f;  // (m, l) of split tid, kept for the weights
+  if (tid < n_sp) {
+    const float2 ml = *reinterpret_cast<const float2*>(base + (int64_t)tid * kPartStride + kD);
+    m0 = ml.x;
+    l0 = ml.y;
+  }
+  float M = m0;
+  for (int i = tid + kMergeThreads; i < n_sp; i += kMergeThreads)
+    M = fmaxf(M, base[(int64_t)i * kPartStride + kD]);
   M = wave_max_xor(M, 64);
   if (lane == 0) sred[w] = M;
   __syncthreads();
   M = sred[0];
 #pragma unroll
   for (int i = 1; i < kMergeWaves; ++i) M = fmaxf(M, sred[i]);
-  float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  float L = 0.0f;
+  float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int i0 = 0; i0 < n_sp; i0 += kMergeThreads) {
     __syncthreads();  // sred / wgt of the previous pass are consumed
     const int i = i0 + tid;
     float wi = 0.0f;
     if (i < n_sp) {
-      const float* p = base + (int64_t)i * kPartStride;
-      wi = exp2_fast(p[kD] - M);
-      L += wi * p[kD + 1];
+      float mi = m0, li = l0;
+      if (i0 != 0) {
+        const float2 ml = *reinterpret_cast<const float2*>(base + (int64_t)i * kPartStride + kD);
+        mi = ml.x;
+        li = ml.y;
+      }
+      wi = exp2_fast(mi - M);
+      L += wi * li;
     }
     wgt[tid] = wi;
     __syncthreads();
     const int cnt = min(kMergeThreads, n_sp - i0);
 #pragma unroll 4
-    for (int k = w; k < cnt; k += kMergeWaves) {
+    for (int k = w + kMergeWaves * half; k < cnt; k += 2 * kMergeWaves) {
       const float wk = wgt[k];
-      const float2 v = *reinterpret_cast<const float2*>(base + (int64_t)(i0 + k) * kPartStride +
-                                                        2 * lane);
-      o0 += wk * v.x;
-      o1 += wk * v.y;
+      const float4 v =
+          *reinterpret_cast<const float4*>(base + (int64_t)(i0 + k) * kPartStride + 4 * c);
+      o.x += wk * v.x;
+      o.y += wk * v.y;
+      o.z += wk * v.z;
+      o.w += wk * v.w;
     }
   }
+  o.x += __shfl_xor(o.x, 32);
+  o.y += __shfl_xor(o.y, 32);
+  o.z += __shfl_xor(o.z, 32);
+  o.w += __shfl_xor(o.w, 32);
   for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
   __syncthreads();
   if (lane == 0) sred[w] = L;
-  red[w][2 * lane] = o0;
-  red[w][2 * lane + 1] = o1;
+  if (half == 0) *reinterpret_cast<float4*>(&red[w][4 * c]) = o;
   __syncthreads();
-  if (w != 0) return;
+  if (w != 0 || half != 0) return;
   L = sred[0];
-  o0 = red[0][2 * lane];
-  o1 = red[0][2 * lane + 1];
+  o = *reinterpret_cast<const float4*>(&red[0][4 * c]);
 #pragma unroll
   for (int i = 1; i < kMergeWaves; ++i) {
     L += sred[i];
-    o0 += red[i][2 * lane];
-    o1 += red[i][2 * lane + 1];
+    const float4 r = *reinterpret_cast<const float4*>(&red[i][4 * c]);
+    o.x += r.x;
+    o.y += r.y;
+    o.z += r.z;
+    o.w += r.w;
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   const int64_t row = ((int64_t)s * a.num_q_heads + qhd) * kD;
   if constexpr (OUT_DTYPE == AMF_DTYPE_F32) {
     float* out = static_cast<float*>(a.out) + row;
-    *reinterpret_cast<float2*>(out + 2 * lane) = float2{o0 * inv, o1 * inv};
+    *reinterpret_cast<float4*>(out + 4 * c) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
   } else {
     constexpr bool BF = OUT_DTYPE == AMF_DTYPE_BF16;
     uint16_t* out = static_cast<uint16_t*>(a.out) + row;
-    const uint32_t packed = (uint32_t)oval<BF>(o0 * inv) | ((uint32_t)oval<BF>(o1 * inv) << 16);
-    *reinterpret_cast<uint32_t*>(out + 2 * lane) = packed;
+    const uint32_t p0 = (uint32_t)oval<BF>(o.x * inv) | ((uint32_t)oval<BF>(o.y * inv) << 16);
+    const uint32_t p1 = (uint32_t)oval<BF>(o.z * inv) | ((uint32_t)oval<BF>(o.w * inv) << 16);
+    *reinterpret_cast<uint2*>(out + 4 * c) = uint2{p0, p1};
   }
 }
 
