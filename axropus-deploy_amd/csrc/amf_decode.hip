@@ -807,7 +807,7 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
 // kTargetWaves waves of work exist when every sequence is max_context_len
 // long, with at most kMaxSplitsPerSeq splits per sequence.
 #ifndef AMF_DECODE_TARGET_WAVES
-#define AMF_DECODE_TARGET_WAVES 32768
+#define AMF_DECODE_TARGET_WAVES 16384
 #endif
 constexpr int64_t kTargetWaves = AMF_DECODE_TARGET_WAVES;
 constexpr int kMaxSplitTokens = 1024;  // 64 pages: one block-table entry per lane
