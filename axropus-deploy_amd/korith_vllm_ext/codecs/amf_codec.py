@@ -238,7 +238,7 @@ class _HipCodec(Codec):
         blob = compressed.meta.get("_blob")
         layout = compressed.meta.get("_layout")
         if blob is None or layout is None:
-            raise ValueError("CompressedKV was not produced by this build's codecs")
+            raise ValueError("CompressedKV was not produced by these codecs")
         P, n, bs, H, D = (layout.n_planes, layout.n_pages, layout.block_size, layout.num_heads,
                           layout.head_dim)
         out = torch.empty(P, n, bs, H, D, dtype=target_dtype, device=blob.device)

@@ -518,8 +518,8 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(the KV hot path shards by layer/head with no exchange; see DESIGN.md).",
+        print("bench.py measures one MI355X: there is no multi-GPU path "
+              "(the KV hot path shards by layer/head with no exchange).",
               file=sys.stderr)
         return 2
     if not torch.cuda.is_available():

@@ -57,7 +57,7 @@ extern "C" {
 /* ---- status codes ------------------------------------------------------ */
 #define AMF_OK                  0
 #define AMF_ERR_INVALID_ARG    (-1)  /* null pointer, negative size, bad enum */
-#define AMF_ERR_UNSUPPORTED    (-2)  /* shape/format this build does not implement */
+#define AMF_ERR_UNSUPPORTED    (-2)  /* shape/format not implemented here */
 #define AMF_ERR_LAUNCH         (-3)  /* the HIP runtime rejected a launch */
 #define AMF_ERR_WORKSPACE      (-4)  /* workspace missing or too small */
 

@@ -1,7 +1,7 @@
 """oracle - CPU restatement of the reference's KV-materialization path.
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py may import this package, and only as the checker
+cpu_baseline leg of bench.py may import this package, and only to check results
 (or, in bench.py, as the timed CPU baseline).  The product path
 (axropus-deploy_amd/) never imports it and has no CPU fallback.
 
@@ -20,5 +20,5 @@ Modules
 
 How each function is pinned (golden vectors, closed forms, brute force) is
 listed in tests/test_oracle_pins.py; a function without such a check would be
-marked "parity unpinned" there and in DESIGN.md.
+marked "parity unpinned" there.
 """
