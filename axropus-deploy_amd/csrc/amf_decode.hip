@@ -711,6 +711,7 @@ __global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
 // several are in flight; the halves and then the waves are summed at the end.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeWaves = kMergeThreads / 64;
+constexpr int kMergePre = 8;  // splits per thread loaded up front (64 per workgroup)
 
 template <int OUT_DTYPE>
 __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(DecodeArgs a) {
@@ -723,6 +724,17 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
   const int ctx = clamp_context(a, s);
   const int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
   const float* base = a.ws + ((int64_t)s * a.num_q_heads + qhd) * a.max_splits * kPartStride;
+  // The accumulators of this thread's first kMergePre splits are loaded
+  // together with the (m, l) words, before the maximum is known, so the merge
+  // waits on memory once (rows clamped into the sequence's splits; a clamped
+  // row is loaded but never added).
+  const int k_first = w + kMergeWaves * half;
+  float4 pre[kMergePre];
+#pragma unroll
+  for (int j = 0; j < kMergePre; ++j) {
+    const int k = max(min(k_first + 2 * kMergeWaves * j, n_sp - 1), 0);
+    pre[j] = *reinterpret_cast<const float4*>(base + (int64_t)k * kPartStride + 4 * c);
+  }
   float m0 = kNegBig, l0 = 0.0f;  // (m, l) of split tid, kept for the weights
   if (tid < n_sp) {
     const float2 ml = *reinterpret_cast<const float2*>(base + (int64_t)tid * kPartStride + kD);
@@ -757,8 +769,23 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
     wgt[tid] = wi;
     __syncthreads();
     const int cnt = min(kMergeThreads, n_sp - i0);
+    int k_from = k_first;
+    if (i0 == 0) {
+#pragma unroll
+      for (int j = 0; j < kMergePre; ++j) {
+        const int k = k_first + 2 * kMergeWaves * j;
+        if (k < cnt) {
+          const float wk = wgt[k];
+          o.x += wk * pre[j].x;
+          o.y += wk * pre[j].y;
+          o.z += wk * pre[j].z;
+          o.w += wk * pre[j].w;
+        }
+      }
+      k_from += 2 * kMergeWaves * kMergePre;
+    }
 #pragma unroll 4
-    for (int k = w + kMergeWaves * half; k < cnt; k += 2 * kMergeWaves) {
+    for (int k = k_from; k < cnt; k += 2 * kMergeWaves) {
       const float wk = wgt[k];
       const float4 v =
           *reinterpret_cast<const float4*>(base + (int64_t)(i0 + k) * kPartStride + 4 * c);
