@@ -18,7 +18,7 @@ import threading
 from collections import OrderedDict
 from typing import Optional, Sequence
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # status codes
 OK = 0
@@ -26,6 +26,9 @@ ERR_INVALID_ARG = -1
 ERR_UNSUPPORTED = -2
 ERR_LAUNCH = -3
 ERR_WORKSPACE = -4
+ERR_FORMAT = -5
+ERR_MISMATCH = -6
+ERR_RUNTIME = -7
 
 ERRFLAG_BLOCK_RANGE = 1
 ERRFLAG_CONTEXT = 2
@@ -54,6 +57,11 @@ _c_i32 = ctypes.c_int32
 _c_i64 = ctypes.c_int64
 _c_f32 = ctypes.c_float
 _c_ptr = ctypes.c_void_p
+_c_u32 = ctypes.c_uint32
+_c_u64 = ctypes.c_uint64
+_p_ptr = ctypes.POINTER(ctypes.c_void_p)
+_p_u32 = ctypes.POINTER(ctypes.c_uint32)
+_p_u64 = ctypes.POINTER(ctypes.c_uint64)
 
 # name -> (restype, argtypes); every symbol declared in include/amf_hip.h.
 SIGNATURES = {
@@ -112,6 +120,29 @@ SIGNATURES = {
         _c_i32,
         [_c_ptr, _c_ptr, _c_ptr, _c_i32, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i32,
          _c_i64, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_ptr],
+    ),
+    "amf_direct_kv_init": (_c_ptr, [_c_u64]),
+    "amf_direct_kv_free": (None, [_c_ptr]),
+    "amf_direct_kv_is_direct_format": (_c_i32, [_c_ptr, _c_u64]),
+    "amf_direct_kv_staging": (_c_i32, [_c_ptr, _c_u64, _p_ptr]),
+    "amf_direct_kv_save": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_u32, _c_u32, _c_u32, _c_u32, _c_u64, _c_ptr,
+         _c_i64, _p_ptr, _p_u64, _c_ptr],
+    ),
+    "amf_direct_kv_restore": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_u64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_u32, _p_u32, _c_ptr],
+    ),
+    "amf_direct_kv_save_pages": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_u32, _c_u32, _c_u32, _c_u32,
+         _c_u64, _c_ptr, _c_i64, _c_ptr, _c_i64, _p_ptr, _p_u64, _c_ptr, _c_ptr],
+    ),
+    "amf_direct_kv_restore_pages": (
+        _c_i32,
+        [_c_ptr, _c_ptr, _c_u64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_u32, _c_ptr,
+         _c_i64, _p_u32, _c_ptr, _c_ptr],
     ),
 }
 

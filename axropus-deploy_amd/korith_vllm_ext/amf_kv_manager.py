@@ -9,14 +9,17 @@ for the same cache contents, including the header's n_kv_heads field, which
 the reference fills from shape[-3] of a gathered [n_blocks, block_size, H, D]
 page stack, i.e. with block_size (amf_kv_manager.py:336-338).
 
-Data movement on the GPU:
-  save    one amf_kv_gather_pages launch gathers the pages of every layer into
-          a device staging buffer laid out as the payload, then one D2H copy
-          into pinned host memory that is written to the file directly;
-  restore the file is read into pinned memory, copied H2D in one transfer,
-          and one amf_kv_scatter_pages launch writes every layer's pages.
-The reference gathers per layer with advanced indexing and copies through
-pageable memory and Python bytes objects (:311-368, 488-523).
+Data movement (libamf_hip.so amf_direct_kv_save_pages / _restore_pages):
+  save    the pages of every layer are gathered into one slot of a two-slot
+          device staging ring while the other slot is copied D2H into the
+          context's pinned blob (header and layer table written natively),
+          and the blob is written to the file in one call;
+  restore the file is read straight into the pinned staging buffer; the
+          header and layer table are validated natively before any copy, then
+          H2D copies of one slot overlap the page scatter of the other.
+Pinned and device staging are kept across calls.  The reference gathers per
+layer with advanced indexing and copies through pageable memory and Python
+bytes objects (:311-368, 488-523).
 """
 
 from __future__ import annotations
@@ -35,6 +38,7 @@ import torch
 import amf_hip
 
 from . import _paged
+from .amf_direct_kv import AmfDirectKv, staging_bytes_for
 
 logger = logging.getLogger(__name__)
 
@@ -148,6 +152,24 @@ class AmfKvManager:
         self._misses = 0
         self._saves = 0
         self._restore_ms = 0.0
+        self._direct: Optional[AmfDirectKv] = None
+        self._staging: Optional[torch.Tensor] = None
+
+    # ---------------------------------------------------------- staging --
+
+    def _direct_ctx(self) -> AmfDirectKv:
+        if self._direct is None:
+            self._direct = AmfDirectKv(0)
+        return self._direct
+
+    def _device_staging(self, device, payload_bytes: int, page_bytes: int) -> torch.Tensor:
+        """The two-slot device ring, reused while it is large enough and on
+        the same device."""
+        want = staging_bytes_for(payload_bytes, page_bytes)
+        st = self._staging
+        if st is None or st.device != device or st.numel() < want:
+            self._staging = torch.empty(want, dtype=torch.uint8, device=device)
+        return self._staging
 
     # -------------------------------------------------------------- keys --
 
@@ -199,31 +221,19 @@ class AmfKvManager:
         else:
             n_blocks, ids = view.pool_pages, None
         page_bytes = view.page_bytes
-        plane_bytes = n_blocks * page_bytes
-        total = 2 * n_layers * plane_bytes
         k0 = _kv_planes(gpu_cache[0])[0]
-        header = struct.pack(
-            _HEADER_FMT, _AMFK_MAGIC, _AMFK_VERSION, n_layers, n_tokens,
-            int(k0.shape[-3]),  # the reference's shape[-3] of the page stack
-            int(k0.shape[-1]), _DTYPE_TAG.get(view.dtype, 0), 0, total,
-            key["model_hash"], key["prefix_hash"])
-        table = b"".join(struct.pack(_LAYER_FMT, 2 * l * plane_bytes, plane_bytes,
-                                     (2 * l + 1) * plane_bytes, plane_bytes)
-                         for l in range(n_layers))
-        # gather every layer's pages into the payload layout, then one D2H copy
-        staging = torch.empty(total, dtype=torch.uint8, device=view.device)
-        outs = [staging.data_ptr() + i * plane_bytes for i in range(2 * n_layers)]
-        _paged.gather_pages(view, ids, outs, page_bytes, n_blocks)
-        host = torch.empty(total, dtype=torch.uint8, pin_memory=True)
-        host.copy_(staging, non_blocking=True)
-        torch.cuda.current_stream(view.device).synchronize()
-        del staging
+        staging = self._device_staging(view.device, 2 * n_layers * n_blocks * page_bytes,
+                                       page_bytes)
+        blob = self._direct_ctx().save_pages(
+            view, _paged._device_ids(ids, view.device), n_blocks, staging,
+            tokens=prompt_tokens,
+            n_kv_heads=int(k0.shape[-3]),  # the reference's shape[-3] of the page stack
+            head_dim=int(k0.shape[-1]), dtype_tag=_DTYPE_TAG.get(view.dtype, 0),
+            model_hash=key["model_hash"])
         tmp_path = kv_path.with_suffix(".kv.tmp")
         try:
             with open(tmp_path, "wb") as f:
-                f.write(header)
-                f.write(table)
-                f.write(memoryview(host.numpy()))
+                f.write(blob)
             os.replace(tmp_path, kv_path)
         except OSError as exc:
             logger.warning("[AMF_VLLM] save: write failed: %s", exc)
@@ -236,7 +246,7 @@ class AmfKvManager:
             logger.warning("[AMF_VLLM] save: tok write failed: %s", exc)
         self._saves += 1
         logger.info("[AMF_VLLM] save: %d layers, %d tokens, %.1f MB in %.0f ms", n_layers,
-                    n_tokens, total / (1 << 20), (time.monotonic() - t0) * 1e3)
+                    n_tokens, len(blob) / (1 << 20), (time.monotonic() - t0) * 1e3)
         return True
 
     # ----------------------------------------------------------- restore --
@@ -252,71 +262,62 @@ class AmfKvManager:
             self._misses += 1
             return 0
         try:
-            size = kv_path.stat().st_size
-            if size < _HEADER_SIZE:
-                logger.warning("[AMF_VLLM] restore: blob too small (%d bytes)", size)
-                self._misses += 1
-                return 0
-            blob = torch.empty(size, dtype=torch.uint8, pin_memory=torch.cuda.is_available())
             with open(kv_path, "rb") as f:
-                f.readinto(memoryview(blob.numpy()))
+                size = os.fstat(f.fileno()).st_size
+                if size < _HEADER_SIZE:
+                    logger.warning("[AMF_VLLM] restore: blob too small (%d bytes)", size)
+                    self._misses += 1
+                    return 0
+                head = f.read(_HEADER_SIZE)
+                (magic, version, n_layers_snap, n_tokens, _heads, _dim, _dtype, _res, _total,
+                 _mh, _ph) = struct.unpack_from(_HEADER_FMT, head, 0)
+                if magic != _AMFK_MAGIC:
+                    logger.warning("[AMF_VLLM] restore: wrong magic 0x%08X (expected AMFK)",
+                                   magic)
+                    self._misses += 1
+                    return 0
+                if version != _AMFK_VERSION:
+                    logger.warning("[AMF_VLLM] restore: version mismatch (got=%d, want=%d)",
+                                   version, _AMFK_VERSION)
+                    self._misses += 1
+                    return 0
+                gpu_cache = self._cache_engine.gpu_cache
+                if n_layers_snap != len(gpu_cache):
+                    logger.warning("[AMF_VLLM] restore: layer count mismatch (snap=%d, ctx=%d)",
+                                   n_layers_snap, len(gpu_cache))
+                    self._misses += 1
+                    return 0
+                if size < _HEADER_SIZE + n_layers_snap * _LAYER_SIZE:
+                    logger.warning("[AMF_VLLM] restore: blob truncated (layer table missing)")
+                    self._misses += 1
+                    return 0
+                if block_table:
+                    # the whole file into the pinned staging buffer; layer
+                    # entries and sizes are validated natively before any copy
+                    view = _paged.cache_view(gpu_cache)
+                    amf_hip.require_device_tensor(gpu_cache[0], "AmfKvManager.restore_kv_state")
+                    _paged.check_block_ids(block_table, view.pool_pages, unique=False)
+                    ctx = self._direct_ctx()
+                    blob = ctx.staging(size)
+                    f.seek(0)
+                    got = f.readinto(blob)
+                    if got != size:
+                        raise OSError(f"short read: {got} of {size} bytes")
         except OSError as exc:
             logger.warning("[AMF_VLLM] restore: read failed: %s", exc)
             self._misses += 1
             return 0
-        raw = memoryview(blob.numpy())
-        (magic, version, n_layers_snap, n_tokens, _heads, _dim, _dtype, _res, _total,
-         _mh, _ph) = struct.unpack_from(_HEADER_FMT, raw, 0)
-        if magic != _AMFK_MAGIC:
-            logger.warning("[AMF_VLLM] restore: wrong magic 0x%08X (expected AMFK)", magic)
-            self._misses += 1
-            return 0
-        if version != _AMFK_VERSION:
-            logger.warning("[AMF_VLLM] restore: version mismatch (got=%d, want=%d)", version,
-                           _AMFK_VERSION)
-            self._misses += 1
-            return 0
-        gpu_cache = self._cache_engine.gpu_cache
-        if n_layers_snap != len(gpu_cache):
-            logger.warning("[AMF_VLLM] restore: layer count mismatch (snap=%d, ctx=%d)",
-                           n_layers_snap, len(gpu_cache))
-            self._misses += 1
-            return 0
-        tbl_end = _HEADER_SIZE + n_layers_snap * _LAYER_SIZE
-        if size < tbl_end:
-            logger.warning("[AMF_VLLM] restore: blob truncated (layer table missing)")
-            self._misses += 1
-            return 0
-        infos = [struct.unpack_from(_LAYER_FMT, raw, _HEADER_SIZE + i * _LAYER_SIZE)
-                 for i in range(n_layers_snap)]
         if block_table:
-            view = _paged.cache_view(gpu_cache)
-            amf_hip.require_device_tensor(gpu_cache[0], "AmfKvManager.restore_kv_state")
-            _paged.check_block_ids(block_table, view.pool_pages, unique=False)
-            n = len(block_table)
-            want = n * view.page_bytes
-            payload_bytes = size - tbl_end
-            ins: List[int] = []
-            planes: List[int] = []
-            for l, (k_off, k_sz, v_off, v_sz) in enumerate(infos):
-                if k_sz == 0 and v_sz == 0:
-                    continue  # a layer without KV (SSM)
-                for off, sz in ((k_off, k_sz), (v_off, v_sz)):
-                    if sz != want or off + sz > payload_bytes:
-                        raise ValueError(
-                            f"layer {l}: snapshot holds {sz} bytes at {off}, the cache needs "
-                            f"{want} for {n} pages")
-                    ins.append(off)
-                planes += view.planes[2 * l:2 * l + 2]
-            if planes:
-                dev = view.device
-                payload = blob.narrow(0, tbl_end, payload_bytes).to(dev, non_blocking=True)
-                base = payload.data_ptr()
-                sub = _paged.CacheView(planes, view.page_stride, view.pool_pages,
-                                       view.block_size, view.num_heads, view.head_dim, view.dtype,
-                                       dev, keep=view.keep)
-                _paged.scatter_pages([base + o for o in ins], view.page_bytes, sub, block_table, n)
-                torch.cuda.current_stream(dev).synchronize()  # the pinned buffer is reused
+            tbl_end = _HEADER_SIZE + n_layers_snap * _LAYER_SIZE
+            staging = self._device_staging(view.device, size - tbl_end, view.page_bytes)
+            try:
+                ctx.restore_pages((ctypes.addressof(ctypes.c_ubyte.from_buffer(blob)), size),
+                                  view, _paged._device_ids(block_table, view.device),
+                                  len(block_table), staging)
+            except amf_hip.AmfHipError as exc:
+                if exc.code in (amf_hip.ERR_FORMAT, amf_hip.ERR_MISMATCH):
+                    raise ValueError(exc.message) from exc
+                raise
         self._hits += 1
         self._restore_ms = (time.monotonic() - t0) * 1e3
         logger.info("[AMF_VLLM] restore: %d layers, %d tokens, %.1f ms", len(gpu_cache),

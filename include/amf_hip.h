@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define AMF_ABI_VERSION 1
+#define AMF_ABI_VERSION 2
 
 /* ---- status codes ------------------------------------------------------ */
 #define AMF_OK                  0
@@ -60,6 +60,9 @@ extern "C" {
 #define AMF_ERR_UNSUPPORTED    (-2)  /* shape/format not implemented here */
 #define AMF_ERR_LAUNCH         (-3)  /* the HIP runtime rejected a launch */
 #define AMF_ERR_WORKSPACE      (-4)  /* workspace missing or too small */
+#define AMF_ERR_FORMAT         (-5)  /* blob is not a valid AMFK snapshot */
+#define AMF_ERR_MISMATCH       (-6)  /* snapshot does not fit the caller's KV tensors */
+#define AMF_ERR_RUNTIME        (-7)  /* a HIP runtime call (allocation, copy, event) failed */
 
 /* bits ORed into *err_flag by kernels */
 #define AMF_ERRFLAG_BLOCK_RANGE 1    /* a block id was outside [0, pool_pages) */
@@ -313,6 +316,115 @@ int amf_dense_attn(const void* q, const void* k, const void* v, int32_t dtype,
                    int64_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                    int64_t q_len, int64_t kv_len, int32_t head_dim,
                    float softmax_scale, void* stream);
+
+/* ---- direct KV snapshots (AMFK blobs through pinned host staging) ----------
+ * The AMFK blob: a 56-byte little-endian header
+ *   u32 magic 0x414D464B ("AMFK"), version 1, n_layers, n_tokens, n_kv_heads,
+ *   head_dim, dtype (AMF_DTYPE_* numbering; 3 = fp8), reserved 0,
+ *   u64 total_kv_bytes, model_hash, prefix_hash (= amf_hash_tokens(tokens)),
+ * then one 32-byte entry per layer, u64 k_offset, k_bytes, v_offset, v_bytes
+ * (offsets from the start of the payload), then the payload: K0 V0 K1 V1 ...
+ * A layer without KV (recurrent/SSM: a zero K or V address) is recorded as
+ * {total, 0, total, 0} and skipped on restore.
+ * (Layout of core/amf_direct_kv.h:35-72; the files of AmfKvManager,
+ * korith_vllm_ext/amf_kv_manager.py:44-64, 327-338, are the same format.)
+ *
+ * A context owns a pinned host staging buffer (hipHostMalloc) that holds the
+ * last saved blob or the blob being restored, and grows by 10% headroom when a
+ * larger one is needed (core/amf_direct_kv.cu:70-93), plus a copy stream of
+ * default priority created on first use on the then-current device.  A
+ * context is not thread-safe; use one per thread or serialise calls.
+ *
+ * Save and restore are stream-ordered on `stream` (NULL = the null stream):
+ * copies start after the work queued there before the call, and a restore's
+ * data is in place for work queued there after it.  Save returns once the
+ * blob is complete in host memory.  Restore returns without a host wait; the
+ * staging buffer stays in use until its copies end, and the context waits
+ * for them before it next hands the buffer out or writes into it.
+ *
+ * Validation is complete before the first copy: a blob that is too short,
+ * has the wrong magic or version, a truncated layer table or a layer entry
+ * outside the payload returns AMF_ERR_FORMAT; a layer count or a layer's
+ * byte size that differs from the caller's returns AMF_ERR_MISMATCH; nothing
+ * is written to the device in either case. */
+typedef struct AmfDirectKvCtx AmfDirectKvCtx;
+
+/* New context; pinned staging of max_kv_bytes (none when 0: no HIP call is
+ * made until the first save/restore).  NULL on failure (amf_last_error()).
+ * Replaces amf_direct_kv_init (core/amf_direct_kv.h:80-84, .cu:98-125). */
+AmfDirectKvCtx* amf_direct_kv_init(uint64_t max_kv_bytes);
+
+/* Frees the context after its outstanding copies end; NULL is ignored.
+ * Replaces amf_direct_kv_free (core/amf_direct_kv.h:86-87, .cu:127-136). */
+void amf_direct_kv_free(AmfDirectKvCtx* ctx);
+
+/* 1 when data holds at least a header and starts with the AMFK magic, else 0.
+ * Replaces amf_direct_kv_is_direct_format (core/amf_direct_kv.h:122-124,
+ * .cu:138-144). */
+int amf_direct_kv_is_direct_format(const uint8_t* data, uint64_t size);
+
+/* The context's pinned staging buffer, grown to at least `bytes`, in
+ * *buf_out: read a snapshot file straight into it, then pass it to a restore
+ * (the role of AmfStore::load_kv_into in core/amf_direct_kv.cu:323-327). */
+int amf_direct_kv_staging(AmfDirectKvCtx* ctx, uint64_t bytes, uint8_t** buf_out);
+
+/* Snapshot n_layers layers of contiguous KV: layer i's K is k_bytes[i] bytes
+ * at device address k_ptrs[i], V likewise (host arrays).  Writes header,
+ * layer table and payload into the staging buffer and returns it in
+ * *blob_out / *blob_bytes_out (valid until the next call on ctx).  dtype is
+ * the header tag; n_kv_heads and head_dim are recorded as given.
+ * Replaces amf_direct_kv_save (core/amf_direct_kv.h:89-104, .cu:158-298)
+ * without the llama.cpp context and store admission: the caller hands the
+ * tensors and stores the blob. */
+int amf_direct_kv_save(AmfDirectKvCtx* ctx, const uint64_t* k_ptrs, const uint64_t* k_bytes,
+                       const uint64_t* v_ptrs, const uint64_t* v_bytes, uint32_t n_layers,
+                       uint32_t n_kv_heads, uint32_t head_dim, uint32_t dtype,
+                       uint64_t model_hash, const int32_t* tokens, int64_t n_tokens,
+                       const uint8_t** blob_out, uint64_t* blob_bytes_out, void* stream);
+
+/* Validate a blob against n_layers layers of contiguous KV (addresses and
+ * sizes as in amf_direct_kv_save) and copy every layer's K and V into them;
+ * *n_tokens_out receives the header's token count.  A blob outside the
+ * staging buffer is first copied into it.
+ * Replaces amf_direct_kv_restore (core/amf_direct_kv.h:106-120,
+ * .cu:302-462) without the llama.cpp cell bookkeeping (the caller marks its
+ * first n_tokens cells used). */
+int amf_direct_kv_restore(AmfDirectKvCtx* ctx, const uint8_t* blob, uint64_t blob_bytes,
+                          const uint64_t* k_ptrs, const uint64_t* k_bytes,
+                          const uint64_t* v_ptrs, const uint64_t* v_bytes, uint32_t n_layers,
+                          uint32_t* n_tokens_out, void* stream);
+
+/* Paged forms, for vLLM's [.., num_blocks, block_size, H, D] caches: the
+ * payload of layer i is the n_pages pages block_ids[0..n_pages) of its K
+ * plane then of its V plane.  cache_planes: host array of 2 * n_layers plane
+ * base addresses (K0, V0, K1, V1, ...; a layer whose two entries are 0 has no
+ * KV); page p of a plane is at plane + p * cache_page_stride; block_ids:
+ * device int32 (NULL = pages 0..n_pages-1).  Pages move through
+ * dev_staging, a caller-owned device buffer of staging_bytes (at least two
+ * pages) used as two slots: while one slot's pages are copied between host
+ * and device on the context's copy stream, the other's are gathered from or
+ * scattered into the cache on `stream`.  Out-of-range block ids are skipped
+ * and flagged in err_flag as in amf_kv_scatter_pages.  With n_pages = 0 a
+ * restore validates the header and layer count only and copies nothing
+ * (AmfKvManager with an empty block table).
+ * Replace the gather + D2H of amf_kv_manager.py:298-368 and the H2D +
+ * scatter of amf_kv_manager.py:488-523, with the header of save_kv_state
+ * (:327-348; n_kv_heads as the caller gives it). */
+int amf_direct_kv_save_pages(AmfDirectKvCtx* ctx, const uint64_t* cache_planes,
+                             int64_t cache_page_stride, const int32_t* block_ids,
+                             int64_t pool_pages, int64_t n_pages, int64_t page_bytes,
+                             uint32_t n_layers, uint32_t n_kv_heads, uint32_t head_dim,
+                             uint32_t dtype, uint64_t model_hash, const int32_t* tokens,
+                             int64_t n_tokens, void* dev_staging, int64_t staging_bytes,
+                             const uint8_t** blob_out, uint64_t* blob_bytes_out,
+                             int32_t* err_flag, void* stream);
+
+int amf_direct_kv_restore_pages(AmfDirectKvCtx* ctx, const uint8_t* blob, uint64_t blob_bytes,
+                                const uint64_t* cache_planes, int64_t cache_page_stride,
+                                const int32_t* block_ids, int64_t pool_pages, int64_t n_pages,
+                                int64_t page_bytes, uint32_t n_layers, void* dev_staging,
+                                int64_t staging_bytes, uint32_t* n_tokens_out,
+                                int32_t* err_flag, void* stream);
 
 #ifdef __cplusplus
 }
