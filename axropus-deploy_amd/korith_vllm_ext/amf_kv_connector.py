@@ -110,6 +110,9 @@ except ImportError:  # vLLM is an optional dependency of this module
         def get_finished(self, finished_req_ids) -> Tuple[Optional[set], Optional[set]]:
             return None, None
 
+        def get_block_ids_with_load_errors(self) -> set:
+            return set()
+
         def request_finished(self, request: Any, block_ids: List[int]):
             return False, None
 
@@ -249,6 +252,7 @@ class AMFKVConnector(KVConnectorBase_V1):
         self._save_layers: Dict[str, Dict[str, Tuple[torch.Tensor, SlotMap]]] = {}
         self._save_slots: Dict[str, SlotMap] = {}  # request id -> its slots, this step
         self._known_hashes: set = set()
+        self._load_error_blocks: set = set()  # blocks of hit requests whose load missed
         self._layer_idx_cache: Dict[str, Optional[int]] = {}
         self._load_stream: Optional[torch.cuda.Stream] = None
         self._layer_events: Dict[str, torch.cuda.Event] = {}
@@ -300,9 +304,10 @@ class AMFKVConnector(KVConnectorBase_V1):
             return 0, False
         prefix_hash = _prefix_hash(token_ids[:n_check])
         pool = self._ensure_pool()
-        hit = prefix_hash in self._known_hashes
-        if not hit and pool is not None:
-            hit = prefix_hash in pool
+        # The pool is the authority when this process has one (an entry may
+        # have been evicted or dropped since it was saved); the saved-hash set
+        # only stands in for it in a scheduler without a GPU.
+        hit = (prefix_hash in pool) if pool is not None else prefix_hash in self._known_hashes
         if not hit:
             return 0, False
         matched = n_check - num_computed_tokens
@@ -392,8 +397,14 @@ class AMFKVConnector(KVConnectorBase_V1):
                 continue
             entry = pool.get(req.prefix_hash)
             if entry is None:
+                # Evicted (or dropped as a failed save) after the scheduler
+                # counted it as a hit: the request's blocks were not filled,
+                # so they are reported for recomputation instead of read.
                 logger.warning("[AMF_CONNECTOR] LOAD MISS prefix=%s (pool has %d entries)",
                                req.prefix_hash[:12], pool.num_prefixes())
+                self._known_hashes.discard(req.prefix_hash)
+                self._load_error_blocks.update(
+                    torch.unique(req.slot_mapping // self._block_size).tolist())
                 continue
             logger.info("[AMF_CONNECTOR] Loading %d tokens for prefix=%s", req.num_tokens,
                         req.prefix_hash[:12])
@@ -509,6 +520,12 @@ class AMFKVConnector(KVConnectorBase_V1):
             else:
                 logger.warning("[AMF_CONNECTOR] Save FAILED for prefix=%s", prefix_hash[:12])
         self._save_layers.clear()
+
+    def get_block_ids_with_load_errors(self) -> set:
+        """Block ids of this step's loads that found no pool entry (vLLM's
+        KVConnectorBase_V1 hook: the scheduler recomputes those tokens)."""
+        out, self._load_error_blocks = self._load_error_blocks, set()
+        return out
 
     @classmethod
     def requires_piecewise_for_cudagraph(cls, extra_config: Dict[str, Any]) -> bool:

@@ -345,13 +345,12 @@ class CompressedVRAMPool:
         """Look up a prefix; a hit updates its recency and hit count."""
         with self._lock:
             entry = self._index.get(prefix_hash)
-            if entry is None:
+            if entry is None or not self._resolve_scales(entry):
                 self._stat_misses += 1
                 return None
             entry.last_hit_ns = time.monotonic_ns()
             entry.hit_count += 1
             self._stat_hits += 1
-            self._resolve_scales(entry)
             return entry
 
     # ------------------------------------------------------- vLLM paths --
@@ -728,14 +727,29 @@ class CompressedVRAMPool:
             self._stat_bytes_stored += entry.nbytes()
             return True
 
-    def _resolve_scales(self, entry: PoolEntry) -> None:
+    def _resolve_scales(self, entry: PoolEntry) -> bool:
         """Per-tensor FP8: turn the asynchronously copied absmax into the
-        reference's Python-double tensor_scale and FP8ScaleSidecar."""
+        reference's Python-double tensor_scale and FP8ScaleSidecar.
+
+        A non-finite layer absmax means the save failed (the single-read
+        kernel writes +inf for a scale group whose cross-workgroup wait gave
+        up, and a cache holding inf has no usable FP8 scale either): the
+        entry is dropped and its spans freed, and False is returned so that
+        the lookup is a miss instead of a restore of inf/NaN pages."""
         if entry.pending_absmax is None:
-            return
+            return True
         host, ev = entry.pending_absmax
         ev.synchronize()
         vals = host.view(torch.float32).tolist()
+        if not all(math.isfinite(v) for v in vals):
+            logger.warning("CompressedVRAMPool: per-tensor FP8 save of %s failed (non-finite "
+                           "absmax in layer %d); entry dropped", entry.prefix_hash[:12],
+                           next(l for l, v in enumerate(vals) if not math.isfinite(v)))
+            entry.pending_absmax = None
+            if self._index.get(entry.prefix_hash) is entry:
+                self._index.pop(entry.prefix_hash)
+            self._release_entry(entry)
+            return False
         blobs = entry.blobs
         for l, blk in enumerate(entry.blocks):
             scale = tensor_scale_from_absmax(vals[l], entry.cache_dtype)
@@ -745,6 +759,7 @@ class CompressedVRAMPool:
             if not isinstance(blobs, _EntryBlobs) or blobs.built(l):
                 blobs[l].tensor_scale = scale
         entry.pending_absmax = None
+        return True
 
     def _fence(self, entry: PoolEntry) -> None:
         """Record the current stream's last launch on the entry's spans (one
@@ -823,6 +838,14 @@ class CompressedVRAMPool:
             stream = torch.cuda.current_stream(self.device)
             for entry in self._index.values():
                 self._wait(entry)
+            # Free runs keep the fences of the entries released into them (a
+            # restore of an evicted entry may still be reading there on a
+            # side stream): the copies below overwrite free space, so they
+            # wait for those launches too.
+            for alloc in self._alloc:
+                for _, _, fences in alloc._runs:
+                    for ev in fences:
+                        stream.wait_event(ev)
             for l in range(self.num_layers):
                 live = sorted((b.block_id, b, e) for e in self._index.values()
                               for b in e.blocks if b.layer_id == l)

@@ -170,6 +170,16 @@ def fallback_fp16_kernel(q: torch.Tensor, k_compressed: Any, v_compressed: Any, 
 # ------------------------------------------------------------ paged path --
 
 
+def _check_buffer(t: torch.Tensor, what: str, dev: torch.device) -> None:
+    """A caller buffer the kernel writes through a raw address: a contiguous
+    tensor on the launch device, or ValueError before any launch."""
+    if not isinstance(t, torch.Tensor) or t.device != dev:
+        raise ValueError(f"paged decode: {what} must be a tensor on {dev}, got "
+                         f"{getattr(t, 'device', type(t).__name__)}")
+    if not t.is_contiguous():
+        raise ValueError(f"paged decode: {what} must be contiguous")
+
+
 def paged_int4_decode(q: torch.Tensor, kv: CompressedKV, block_tables: torch.Tensor,
                       context_lens: torch.Tensor, *, scale: Optional[float] = None,
                       max_context_len: Optional[int] = None, out: Optional[torch.Tensor] = None,
@@ -180,9 +190,12 @@ def paged_int4_decode(q: torch.Tensor, kv: CompressedKV, block_tables: torch.Ten
     q [num_seqs, Hq, D] or [num_seqs, Hq, 1, D] (bf16/fp16); kv the
     CompressedKV of a layer's page tensor [2, pool_pages, 16, Hkv, D] (K and V
     planes); block_tables int32 [num_seqs, max_pages] of pool page ids;
-    context_lens int32 [num_seqs].  max_context_len (>= every context length;
-    computed from context_lens when omitted, which reads it back to the host)
-    sizes the split-K workspace."""
+    context_lens int32 [num_seqs].  max_context_len (>= every context length)
+    sizes the grid and the split-K workspace; when omitted it is the block
+    table's capacity, block_tables.shape[1] * 16, so no value is read back
+    from the device.  `out` (contiguous [num_seqs, Hq, D] on the pool's
+    device, bf16/fp16/fp32) and `workspace` (contiguous, on that device) are
+    checked before the launch; a bad one raises ValueError."""
     layout = kv.meta.get("_layout") if isinstance(kv, CompressedKV) else None
     if layout is None or kv.format != FMT_INT4_ASYM_G32 or layout.n_planes != 2:
         raise ValueError("paged decode needs the int4_asym_g32 CompressedKV of a layer page "
@@ -207,12 +220,22 @@ def paged_int4_decode(q: torch.Tensor, kv: CompressedKV, block_tables: torch.Ten
         raise ValueError(f"block_tables {tuple(bt.shape)} / context_lens {tuple(cl.shape)} do "
                          f"not match {S} sequences")
     if max_context_len is None:
-        max_context_len = int(cl.max()) if S else 0
-    odt = out_dtype or q3.dtype
+        max_context_len = int(bt.shape[1]) * layout.block_size
+    odt = out_dtype or (out.dtype if out is not None else q3.dtype)
+    if odt not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"paged decode: output dtype {odt} is not bf16/fp16/fp32")
     if out is None:
         out = torch.empty(S, Hq, D, dtype=odt, device=dev)
-    amf_hip.require_device_tensor(out, "paged decode out")
+    else:
+        _check_buffer(out, "out", dev)
+        if tuple(out.shape) != (S, Hq, D) and tuple(out.shape) != (S, Hq, 1, D):
+            raise ValueError(f"paged decode: out has shape {tuple(out.shape)}, needs "
+                             f"({S}, {Hq}, {D})")
+        if out.dtype != odt:
+            raise ValueError(f"paged decode: out is {out.dtype}, out_dtype asks for {odt}")
     wsb = amf_hip.decode_workspace_bytes(S, Hq, layout.num_heads, D, max_context_len)
+    if workspace is not None:
+        _check_buffer(workspace, "workspace", dev)
     if workspace is None or workspace.numel() * workspace.element_size() < wsb:
         workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=dev)
     algos = {"auto": amf_hip.DECODE_AUTO, "valu": amf_hip.DECODE_VALU, "mfma": amf_hip.DECODE_MFMA}

@@ -7,19 +7,34 @@ stored as fp8_e4m3_ph (per-(page, head) fp32 scale) is dequantized and
 scattered into a bf16 paged cache of 8192 pages through a seeded random block
 table.  One step = one restore of all 32 layers (one kernel launch).
 
-Also reported (same JSON line):
-  int4_restore : int4_asym_g32 restore, 2048-page prefix into a 16384-page pool
-  int4_decode  : paged GQA decode over INT4 KV, batch 32, Hq 32 / Hkv 8,
-                 contexts U[1024, 32768], one layer call
+Every workload of the benchmark spec has a section on the same JSON line:
+  c1_raw_qwen2_0_5b : raw page gather and scatter, 24 layers x 128 pages of
+                      4 KiB, rotated over 24 disjoint page sets (1.15 GB) so
+                      the 256 MB memory-side cache cannot hold them
+  c2_fp8_llama3_8b  : the headline restore, its save, the pool API
+  c3_int4_llama3_8b : int4_asym_g32 restore and save, 2048 pages, 16384-page pool
+  c4_decode_llama3_8b : paged GQA decode over INT4 KV, batch 32, Hq 32 / Hkv 8,
+                      contexts U[1024, 32768], one layer call
+  c5_llama3_70b     : FP8 restore of 80 layers x 8192 pages, decode at batch 8
+                      x 131072 tokens, Hq 64 / Hkv 8
+plus the reference's own codec formats, the connector and the AMFK tier.
 
-GB/s = algorithmic bytes / mean kernel time (HIP events on the launch stream,
-1 GB = 1e9 B).  Algorithmic bytes: restore = codes + params read + cache
-bytes written; decode = 1280 B per context token (8 heads x (2 x 64 B codes
-+ 2 x 16 B params)).  The CPU baseline is the reference's PyTorch op sequence
-restated on the host (oracle/), timed on a bounded sample.
+GPU times are HIP events on the launch stream: `ms` is the mean over the
+timed launches (events around the whole timed region), `median_ms` the
+median of per-launch event pairs.  GB/s = algorithmic bytes / median_ms
+(1 GB = 1e9 B); the headline `value` uses the mean (= ms_per_step).
+Algorithmic bytes: restore/save = codes + params read or written + cache
+bytes written or read; raw copy = page bytes read + written; decode = 1280 B
+per context token (8 heads x (2 x 64 B codes + 2 x 16 B params)).
+
+Each section's `cpu` entry is the reference's PyTorch op sequence restated
+on the host (oracle/), timed on all CPUs of this process's affinity on a
+bounded sample after the GPU work, and checked against the GPU result of the
+same inputs (bit-exact for copies and codecs, max-abs / mean-rel for
+attention).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
-       python bench.py --profile {fp8_restore,int4_restore,decode_mfma,decode_valu}
+       python bench.py --profile {fp8_restore,int4_restore,decode_mfma,...}
 """
 
 from __future__ import annotations
@@ -67,19 +82,77 @@ def seeded_table(pool: int, n: int, seed: int) -> torch.Tensor:
     return torch.randperm(pool, generator=torch.Generator().manual_seed(seed))[:n].to(torch.int32)
 
 
-def time_launches(fn, steps: int, warmup: int) -> float:
-    """Mean milliseconds per call of fn (HIP events on torch's current stream)."""
+class Timing:
+    """Mean (whole timed region) and median (per-launch) milliseconds."""
+
+    def __init__(self, mean_ms: float, median_ms: float, n: int):
+        self.mean_ms, self.median_ms, self.n = mean_ms, median_ms, n
+
+    def leg(self, algo_bytes: int, **extra) -> dict:
+        gbs = algo_bytes / (self.median_ms * 1e-3) / 1e9
+        d = {"ms": round(self.mean_ms, 5), "median_ms": round(self.median_ms, 5),
+             "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+             "algo_bytes": int(algo_bytes)}
+        d.update(extra)
+        return d
+
+
+def time_launches(fn, steps: int, warmup: int) -> Timing:
+    """fn launched `steps` times on torch's current stream after `warmup`
+    untimed launches; events around every launch and around the region."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(steps):
+    for a, b in evs:
+        a.record()
         fn()
+        b.record()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    per = [a.elapsed_time(b) for a, b in evs]
+    return Timing(start.elapsed_time(end) / steps, statistics.median(per), steps)
+
+
+def cpu_time(run, min_runs: int = 3, min_seconds: float = 4.0):
+    """Median seconds of run() over >= min_runs runs and >= min_seconds."""
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or time.perf_counter() - t_start < min_seconds:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times), time.perf_counter() - t_start
+
+
+def host_info() -> dict:
+    """CPU model, the threads torch uses (this process's CPU affinity), torch."""
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"cpu": model, "threads": int(n or 1), "torch": torch.__version__}
+
+
+def bits_equal(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return a.shape == b.shape and torch.equal(a.contiguous().view(torch.int16),
+                                              b.contiguous().view(torch.int16))
+
+
+def attn_errors(got: torch.Tensor, ref: torch.Tensor) -> dict:
+    """max |a - b| and mean-rel = sum |a - b| / sum |b|."""
+    d = (got.double() - ref.double()).abs()
+    return {"max_abs": float(d.max()), "mean_rel": float(d.sum() / ref.double().abs().sum())}
 
 
 # ----------------------------------------------------------------- restore --
@@ -117,58 +190,59 @@ class RestoreCase:
         written = self.layers * 2 * self.pages * lay.page_elems * 2
         return read + written
 
-    def cpu_baseline(self, sample_layers: int, min_seconds: float = 10.0):
+    def cpu_baseline(self, sample_layers: int, min_runs: int = 3, min_seconds: float = 4.0):
         """The reference restore op sequence on the host for `sample_layers`
-        layers: per layer decompress_to(bf16) then chunked k_all[ids] = src
-        (compressed_vram_pool.py:579-606), on a host copy of the blobs.
+        layers: per layer decompress_to(bf16) then 512-block chunked
+        k_all[ids] = src (compressed_vram_pool.py:579-606), on a host copy of
+        the blobs.
 
-        Copies the inputs to the host now and returns a callable that times
-        the restore when called, so the CPU work can run after every GPU
-        measurement instead of idling the GPU between them."""
+        Copies the inputs and the GPU's restored pages of those layers to the
+        host now (call after a GPU restore) and returns a callable that times
+        the CPU restore and checks it bit for bit against the GPU's pages, so
+        the CPU work runs after every GPU measurement."""
         from oracle import codecs as oc
 
         lay = self.layout
         ids = self.ids.long()
         blobs = [self.blobs[l].cpu() for l in range(sample_layers)]
-        cache = [torch.empty(2, self.pool, 16, self.heads, self.head_dim, dtype=torch.bfloat16)
-                 for _ in range(sample_layers)]
-        for c in cache:
-            c.zero_()
-
-        def run():
-            for l, blob in enumerate(blobs):
-                codes = blob[:lay.data_bytes].view(2, self.pages, 16, self.heads, self.head_dim)
-                if self.fmt == "fp8_e4m3_ph":
-                    sc = torch.stack([blob[lay.param_offset(p):lay.param_offset(p) + lay.plane_param_bytes]
-                                      .view(torch.float32).view(self.pages, self.heads) for p in range(2)])
-                    kv = oc.fp8_ph_decompress(codes, sc, torch.bfloat16)
-                else:
-                    cpl = lay.plane_code_bytes
-                    c = torch.stack([blob[lay.code_offset(p):lay.code_offset(p) + cpl]
-                                     .view(self.pages, -1) for p in range(2)])
-                    pr = torch.stack([blob[lay.param_offset(p):lay.param_offset(p) + lay.plane_param_bytes]
-                                      .view(torch.int32).view(self.pages, -1).to(torch.int64) & 0xFFFFFFFF
-                                      for p in range(2)])
-                    kv = oc.int4_asym_decompress(c, pr, 16, self.heads, self.head_dim, torch.bfloat16)
-                for start in range(0, self.pages, 512):
-                    end = min(start + 512, self.pages)
-                    cache[l][0][ids[start:end]] = kv[0][start:end]
-                    cache[l][1][ids[start:end]] = kv[1][start:end]
-
-        sample_bytes = self.algo_bytes * sample_layers / self.layers
+        gpu_pages = [self.cache[l][:, ids.to(DEV)].cpu() for l in range(sample_layers)]
+        pool, heads, hd, pages, fmt = self.pool, self.heads, self.head_dim, self.pages, self.fmt
+        sample_bytes = self.algo_bytes * sample_layers // self.layers
         n_layers = self.layers
 
         def timed() -> dict:
-            times = []
-            t_start = time.perf_counter()
-            while len(times) < 3 or time.perf_counter() - t_start < min_seconds:
-                t0 = time.perf_counter()
-                run()
-                times.append(time.perf_counter() - t0)
-            t = statistics.median(times)
-            return {"value": sample_bytes / t / 1e9, "unit": "GB/s", "seconds": t,
+            cache = [torch.zeros(2, pool, 16, heads, hd, dtype=torch.bfloat16)
+                     for _ in range(sample_layers)]
+
+            def run():
+                for l, blob in enumerate(blobs):
+                    if fmt == "fp8_e4m3_ph":
+                        codes = blob[:lay.data_bytes].view(2, pages, 16, heads, hd)
+                        sc = torch.stack([blob[lay.param_offset(p):lay.param_offset(p) +
+                                               lay.plane_param_bytes]
+                                          .view(torch.float32).view(pages, heads)
+                                          for p in range(2)])
+                        kv = oc.fp8_ph_decompress(codes, sc, torch.bfloat16)
+                    else:
+                        cpl = lay.plane_code_bytes
+                        c = torch.stack([blob[lay.code_offset(p):lay.code_offset(p) + cpl]
+                                         .view(pages, -1) for p in range(2)])
+                        pr = torch.stack([blob[lay.param_offset(p):lay.param_offset(p) +
+                                               lay.plane_param_bytes]
+                                          .view(torch.int32).view(pages, -1).to(torch.int64)
+                                          & 0xFFFFFFFF for p in range(2)])
+                        kv = oc.int4_asym_decompress(c, pr, 16, heads, hd, torch.bfloat16)
+                    for start in range(0, pages, 512):
+                        end = min(start + 512, pages)
+                        cache[l][0][ids[start:end]] = kv[0][start:end]
+                        cache[l][1][ids[start:end]] = kv[1][start:end]
+
+            t, runs, total = cpu_time(run, min_runs, min_seconds)
+            same = all(bits_equal(cache[l][:, ids], gpu_pages[l]) for l in range(sample_layers))
+            return {"GB/s": round(sample_bytes / t / 1e9, 3), "seconds": round(t, 4),
                     "sample": f"restore of {sample_layers} of {n_layers} layers, median of "
-                              f"{len(times)} runs ({time.perf_counter() - t_start:.1f} s total)"}
+                              f"{runs} runs ({total:.1f} s)",
+                    "parity_vs_gpu": "bit-exact" if same else "MISMATCH"}
 
         return timed
 
@@ -348,7 +422,7 @@ class ConnectorCase:
         load_ms = wall(lambda: self.load(lmeta))
         algo = self.algo_bytes()
         fn, moved, keep = self.slot_launch()
-        slot_ms = time_launches(fn, steps, warmup)
+        slot_ms = time_launches(fn, steps, warmup).median_ms
         del keep
         return {"workload": "connector_llama3_8b_8k", "format": self.fmt,
                 "tokens": self.tokens, "layers": self.layers,
@@ -438,38 +512,287 @@ class DecodeCase:
         return 1280 * self.sum_ctx * self.kv_heads // 8
 
 
+    def cpu_fallback(self, sample_seqs: int, min_runs: int = 3, min_seconds: float = 4.0):
+        """The reference's INT4 decode path on the host for the first
+        `sample_seqs` sequences: decompress the sequence's pages to bf16
+        (codecs' decompress_to; here the int4_asym_g32 restatement), repeat the
+        KV heads for GQA, then matmul -> softmax -> matmul in bf16
+        (kernels/dispatch.py:117-152).  Copies the pages and this GPU call's
+        output rows to the host now; the returned callable times the CPU path
+        and reports its distance from the GPU output."""
+        from oracle import attention as oatt
+        from oracle import codecs as oc
+
+        lay = self.layout
+        D, H, R = self.D, self.kv_heads, self.q_heads // self.kv_heads
+        torch.cuda.synchronize()
+        gpu_out = self.out[:sample_seqs].float().cpu()
+        q = self.q[:sample_seqs].cpu()
+        seqs = []
+        cpp = lay.code_bytes_per_page
+        ppw = lay.plane_param_bytes // self.pool // 4
+        for b in range(sample_seqs):
+            ctx = int(self.ctx[b])
+            n = (ctx + 15) // 16
+            pages = self.bt[b, :n].long()
+            codes = torch.stack([self.blob[lay.code_offset(p):lay.code_offset(p) + lay.plane_code_bytes]
+                                 .view(self.pool, cpp)[pages].cpu() for p in range(2)])
+            params = torch.stack([self.blob[lay.param_offset(p):lay.param_offset(p) +
+                                            lay.plane_param_bytes]
+                                  .view(torch.int32).view(self.pool, ppw)[pages].cpu()
+                                  .to(torch.int64) & 0xFFFFFFFF for p in range(2)])
+            seqs.append((ctx, n, codes, params))
+        sum_ctx = sum(c for c, _, _, _ in seqs)
+        out = torch.empty(sample_seqs, self.q_heads, D, dtype=torch.bfloat16)
+        batch = self.batch
+
+        def run():
+            for b, (ctx, n, codes, params) in enumerate(seqs):
+                kv = oc.int4_asym_decompress(codes, params, 16, H, D, torch.bfloat16)
+                k = kv[0].reshape(n * 16, H, D)[:ctx].permute(1, 0, 2)
+                v = kv[1].reshape(n * 16, H, D)[:ctx].permute(1, 0, 2)
+                k = k.repeat_interleave(R, dim=0)[None]
+                v = v.repeat_interleave(R, dim=0)[None].contiguous()
+                out[b] = oatt.fallback_attention(q[b][None, :, None, :], k, v)[0, :, 0]
+
+        def timed() -> dict:
+            t, runs, total = cpu_time(run, min_runs, min_seconds)
+            err = attn_errors(gpu_out, out.float())
+            return {"kv_tok_per_s": round(sum_ctx / t, 1),
+                    "GB/s": round(1280 * H // 8 * sum_ctx / t / 1e9, 3),
+                    "queries_per_s_per_layer": round(sample_seqs / t, 3), "seconds": round(t, 4),
+                    "sample": f"{sample_seqs} of {batch} sequences ({sum_ctx} context "
+                              f"tokens), median of {runs} runs ({total:.1f} s)",
+                    "gpu_vs_cpu_fallback": {k: float(f"{v:.3e}") for k, v in err.items()}}
+
+        return timed
+
+
+class RawCase:
+    """Raw page gather and scatter at the Qwen2-0.5B KV shape: 24 layers of
+    [2, 4096, 16, 2, 64] bf16 (4 KiB pages), a 128-page prefix gathered
+    through a seeded random block table, then scattered into a different
+    seeded random set of 128 pages of a second cache.  Launch r uses the r-th
+    of `rotations` disjoint page sets and its own dense buffer, so that the
+    data of consecutive launches (1.15 GB over 24 rotations) does not fit the
+    256 MB memory-side cache."""
+
+    L, POOL, PAGES, H, D = 24, 4096, 128, 2, 64
+
+    def __init__(self, rotations: int = 24, seed: int = 1):
+        from korith_vllm_ext import _paged
+        import amf_hip
+
+        L, pool, n, H, D = self.L, self.POOL, self.PAGES, self.H, self.D
+        self.rot = rotations
+        self.src = [device_kv((2, pool, 16, H, D), D, seed * 100 + l, outliers=False)
+                    for l in range(L)]
+        self.dst = [torch.zeros_like(c) for c in self.src]
+        pa = torch.randperm(pool, generator=torch.Generator().manual_seed(seed))
+        pb = torch.randperm(pool, generator=torch.Generator().manual_seed(seed + 1))
+        self.ids_g = [pa[r * n:(r + 1) * n].to(torch.int32) for r in range(rotations)]
+        self.ids_s = [pb[r * n:(r + 1) * n].to(torch.int32) for r in range(rotations)]
+        self.bufs = torch.empty(rotations, 2 * L, n, 16, H, D, dtype=torch.bfloat16, device=DEV)
+        sview, dview = _paged.cache_view(self.src), _paged.cache_view(self.dst)
+        self.page_bytes = sview.page_bytes
+        self.stride = sview.page_stride
+        self.src_tab = amf_hip.address_table(sview.planes, DEV)
+        self.dst_tab = amf_hip.address_table(dview.planes, DEV)
+        self.buf_tabs = [amf_hip.address_table([self.bufs[r, i].data_ptr() for i in range(2 * L)],
+                                               DEV) for r in range(rotations)]
+        self.dg = [i.to(DEV) for i in self.ids_g]
+        self.ds = [i.to(DEV) for i in self.ids_s]
+        self.lib = amf_hip.load()
+        self.amf_hip = amf_hip
+        self._r = 0
+        torch.cuda.synchronize()
+
+    @property
+    def algo_bytes(self) -> int:
+        return 2 * 2 * self.L * self.PAGES * self.page_bytes
+
+    def gather(self, r: int) -> None:
+        rc = self.lib.amf_kv_gather_pages(self.src_tab.data_ptr(), self.stride,
+                                          self.dg[r].data_ptr(), self.POOL,
+                                          self.buf_tabs[r].data_ptr(), self.page_bytes,
+                                          2 * self.L, self.PAGES, self.page_bytes, None,
+                                          self.amf_hip.stream_handle(DEV))
+        self.amf_hip.check("amf_kv_gather_pages", rc)
+
+    def scatter(self, r: int) -> None:
+        rc = self.lib.amf_kv_scatter_pages(self.buf_tabs[r].data_ptr(), self.page_bytes,
+                                           self.dst_tab.data_ptr(), self.stride,
+                                           self.ds[r].data_ptr(), self.POOL, 2 * self.L,
+                                           self.PAGES, self.page_bytes, None,
+                                           self.amf_hip.stream_handle(DEV))
+        self.amf_hip.check("amf_kv_scatter_pages", rc)
+
+    def rotating(self, op):
+        def fn():
+            op(self._r)
+            self._r = (self._r + 1) % self.rot
+        return fn
+
+    def cpu_baseline(self, min_runs: int = 3, min_seconds: float = 3.0):
+        """The reference op sequence on the host: per layer k_all[ids] /
+        v_all[ids] then .contiguous() (amf_kv_manager.py:311-318), and
+        k_all[ids] = src into the second cache (compressed_vram_pool.py:
+        599-606), for rotation 0 of the GPU run; checked bit for bit against
+        the GPU's gathered buffer and scattered pages."""
+        torch.cuda.synchronize()
+        src = [c.cpu() for c in self.src]
+        dst = [torch.zeros_like(c) for c in src]
+        gi, si = self.ids_g[0].long(), self.ids_s[0].long()
+        gpu_buf = self.bufs[0].cpu()
+        gpu_dst = [c[:, si.to(DEV)].cpu() for c in self.dst]
+        L, algo = self.L, self.algo_bytes
+        outs = [None] * (2 * L)
+
+        def gather():
+            for l, c in enumerate(src):
+                ids = torch.tensor(gi.tolist(), dtype=torch.long)
+                outs[2 * l] = c[0][ids].contiguous()
+                outs[2 * l + 1] = c[1][ids].contiguous()
+
+        def scatter():
+            for l, c in enumerate(dst):
+                ids = torch.tensor(si.tolist(), dtype=torch.long)
+                c[0][ids] = outs[2 * l]
+                c[1][ids] = outs[2 * l + 1]
+
+        def timed() -> dict:
+            tg, ng, _ = cpu_time(gather, min_runs, min_seconds)
+            ts, ns, _ = cpu_time(scatter, min_runs, min_seconds)
+            same = all(bits_equal(outs[i], gpu_buf[i]) for i in range(2 * L)) and all(
+                bits_equal(dst[l][:, si], gpu_dst[l]) for l in range(L))
+            return {"gather_GB/s": round(algo / tg / 1e9, 3),
+                    "scatter_GB/s": round(algo / ts / 1e9, 3),
+                    "gather_seconds": round(tg, 5), "scatter_seconds": round(ts, 5),
+                    "sample": f"the whole workload (rotation 0), median of {ng} / {ns} runs",
+                    "parity_vs_gpu": "bit-exact" if same else "MISMATCH"}
+
+        return timed
+
+    def free(self):
+        del self.src, self.dst, self.bufs
+        torch.cuda.empty_cache()
+
+
+class AmfkCase:
+    """AmfKvManager save_kv_state / restore_kv_state (AMFK files) at the
+    Qwen2-0.5B shape of RawCase: the 128-page prefix of all 24 layers
+    (24 MiB payload) saved to a file and restored into other pages of a
+    second cache.  Wall clock per call, file in /dev/shm when present (the
+    page cache otherwise), plus the native restore alone (pinned blob ->
+    staging ring -> pages) for the PCIe-bound part."""
+
+    def __init__(self, raw: RawCase):
+        import tempfile
+
+        from korith_vllm_ext.amf_kv_manager import AmfKvManager
+
+        class _Engine:
+            def __init__(self, caches):
+                self.gpu_cache = caches
+
+        class _Cfg:
+            max_model_len = 32768
+
+        base = "/dev/shm" if os.path.isdir("/dev/shm") else None
+        self.dir = tempfile.mkdtemp(prefix="amfk_bench_", dir=base)
+        self.raw = raw
+        self.save_mgr = AmfKvManager(_Engine(raw.src), self.dir, _Cfg())
+        self.load_mgr = AmfKvManager(_Engine(raw.dst), self.dir, _Cfg())
+        self.toks = list(range(raw.PAGES * 16))
+
+    def run(self, steps: int, warmup: int) -> dict:
+        from korith_vllm_ext import _paged
+
+        raw = self.raw
+        src, dst = raw.ids_g[0].tolist(), raw.ids_s[0].tolist()
+
+        def wall(fn, n):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(n):
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                ts.append(time.perf_counter() - t0)
+            return statistics.median(ts) * 1e3
+
+        n = max(3, min(steps, 10))
+        save_ms = wall(lambda: self.save_mgr.save_kv_state(self.toks, src), n)
+        load_ms = wall(lambda: self.load_mgr.restore_kv_state(self.toks, dst), n)
+        torch.cuda.synchronize()
+        si = raw.ids_s[0].long().to(DEV)
+        gi = raw.ids_g[0].long().to(DEV)
+        same = all(bits_equal(raw.dst[l][:, si], raw.src[l][:, gi]) for l in range(raw.L))
+        # the native part alone: the blob already in pinned memory
+        mgr = self.load_mgr
+        path = mgr._kv_filename(mgr.compute_amf_key(self.toks))
+        data = path.read_bytes()
+        ctx = mgr._direct_ctx()
+        blob = ctx.staging(len(data))
+        blob[:] = data
+        view = _paged.cache_view(raw.dst)
+        ids = raw.ds[0]
+        staging = mgr._staging
+        native_ms = wall(lambda: ctx.restore_pages(blob, view, ids, raw.PAGES, staging), n)
+        payload = len(data) - 56 - 32 * raw.L
+        return {"workload": "amfk_qwen2_0_5b_2k", "payload_bytes": payload,
+                "save_kv_state_ms": round(save_ms, 4),
+                "save_GB/s": round(payload / save_ms / 1e6, 2),
+                "restore_kv_state_ms": round(load_ms, 4),
+                "restore_GB/s": round(payload / load_ms / 1e6, 2),
+                "native_restore_pages_ms": round(native_ms, 4),
+                "native_restore_GB/s": round(payload / native_ms / 1e6, 2),
+                "staging_ring_bytes": int(staging.numel()),
+                "file_dir": os.path.dirname(self.dir),
+                "parity": "bit-exact" if same else "MISMATCH"}
+
+    def free(self):
+        import shutil
+
+        shutil.rmtree(self.dir, ignore_errors=True)
+
+
 # -------------------------------------------------------------------- main --
 
 
-def long_context_70b(steps: int, warmup: int) -> dict:
+def long_context_70b(steps: int, warmup: int, cpu_jobs: list, want_cpu: bool) -> dict:
     """Llama-3-70B share on one GPU: FP8-PH restore of a 131072-token prefix
     (80 layers x 8192 pages, ~21.5 GB of blobs into a 43 GB bf16 cache) and
     INT4 decode at batch 8 x 131072 tokens, 64 query heads (GQA 8).  Skipped
-    when the device lacks the ~70 GB it needs."""
+    when the device lacks the ~70 GB it needs.  CPU: 2 of 80 layers of the
+    restore and 1 of 8 decode sequences (the spec allows a layer subset)."""
     free, _ = torch.cuda.mem_get_info()
     if free < 80 * (1 << 30):
         log(f"70b workloads skipped: {free / 2**30:.0f} GiB free")
-        return {"fp8_restore_70b": None, "decode_70b": None}
+        return {"skipped": f"{free / 2**30:.0f} GiB free"}
     out = {}
     log("70b fp8 restore: building inputs")
     case = RestoreCase("fp8_e4m3_ph", 80, 8, 128, 8192, 8192, 5)
-    ms = time_launches(case.launch.launch, max(3, steps // 4), warmup)
-    gbs = case.algo_bytes / (ms * 1e-3) / 1e9
-    out["fp8_restore_70b"] = {"workload": "fp8_restore_llama3_70b_131k", "ms": round(ms, 4),
-                              "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                              "algo_bytes": case.algo_bytes}
-    log(f"70b fp8 restore: {ms:.3f} ms, {gbs:.1f} GB/s")
+    t = time_launches(case.launch.launch, max(5, steps // 2), warmup)
+    out["fp8_restore"] = t.leg(case.algo_bytes, workload="fp8_restore_llama3_70b_131k")
+    log(f"70b fp8 restore: {out['fp8_restore']}")
+    if want_cpu:
+        cpu_jobs.append(("c5_llama3_70b", "cpu_fp8_restore", case.cpu_baseline(2, 1, 2.0)))
     case.free()
     del case
     log("70b decode: building inputs")
     dc = DecodeCase(8, 64, 8, 131072, 131072, 6)
-    msd = time_launches(lambda: dc.launch(amf_hip_module().DECODE_MFMA), steps, warmup)
-    gd = dc.algo_bytes / (msd * 1e-3) / 1e9
-    out["decode_70b"] = {"workload": "decode_llama3_70b_b8_131k", "ms_per_layer_call": round(msd, 5),
-                         "tok_per_s_per_layer": round(dc.batch / (msd * 1e-3), 1),
-                         "tok_per_s_model_80_layers": round(dc.batch / (80 * msd * 1e-3), 1),
-                         "GB/s": round(gd, 1), "frac": round(gd / HBM_PEAK_GBS, 4)}
-    log(f"70b decode: {msd:.4f} ms, {gd:.1f} GB/s")
+    td = time_launches(lambda: dc.launch(amf_hip_module().DECODE_MFMA), steps, warmup)
+    msd = td.median_ms
+    out["decode"] = td.leg(dc.algo_bytes, workload="decode_llama3_70b_b8_131k",
+                           tok_per_s_per_layer=round(dc.batch / (msd * 1e-3), 1),
+                           tok_per_s_model_80_layers=round(dc.batch / (80 * msd * 1e-3), 1),
+                           kv_tok_per_s=round(dc.sum_ctx / (msd * 1e-3), 1))
+    log(f"70b decode: {out['decode']}")
+    if want_cpu:
+        cpu_jobs.append(("c5_llama3_70b", "cpu_decode_fallback", dc.cpu_fallback(1, 1, 1.0)))
     del dc
     torch.cuda.empty_cache()
     return out
@@ -496,9 +819,65 @@ def profiled_traffic(name: str):
     return None
 
 
-def cpu_threads() -> int:
-    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    return max(1, min(int(n or 1), 16))
+def run_profile(name: str, steps: int, warmup: int) -> int:
+    """One kernel loop, for rocprofv3."""
+    import amf_hip
+
+    if name == "copy":
+        # Calibration for the HBM byte counters: a raw page copy of exactly
+        # 1 GiB read + 1 GiB written (2 planes of 16384 pages of 32 KiB).
+        from korith_vllm_ext import _paged
+
+        src = torch.empty(2, 16384, 16, 8, 128, dtype=torch.bfloat16, device=DEV).fill_(1.0)
+        dst = torch.empty_like(src)
+        view = _paged.cache_view([src])
+        fn = lambda: _paged.gather_pages(view, None, [dst[0].data_ptr(), dst[1].data_ptr()],
+                                         view.page_bytes, 16384)
+        t = time_launches(fn, steps, warmup)
+        log(f"copy: {t.mean_ms:.4f} ms/launch, 1 GiB read + 1 GiB written per launch, "
+            f"{2 * 2**30 / t.mean_ms / 1e6:.1f} GB/s")
+        return 0
+    if name in ("raw_gather", "raw_scatter"):
+        rc = RawCase()
+        t = time_launches(rc.rotating(rc.gather if name == "raw_gather" else rc.scatter), steps,
+                          warmup)
+        log(f"{name}: {t.leg(rc.algo_bytes)}")
+        return 0
+    if name == "slot_copy":
+        cc = ConnectorCase()
+        fn, moved, keep = cc.slot_launch()
+        t = time_launches(fn, steps, warmup)
+        log(f"slot_copy: {t.mean_ms:.4f} ms/launch, {moved / t.mean_ms / 1e6:.1f} GB/s")
+        return 0
+    if name == "fp8_restore_70b":
+        case = RestoreCase("fp8_e4m3_ph", 80, 8, 128, 8192, 8192, 5)
+        t = time_launches(case.launch.launch, steps, warmup)
+        log(f"{name}: {t.leg(case.algo_bytes)}")
+        return 0
+    if name == "decode_70b":
+        case = DecodeCase(8, 64, 8, 131072, 131072, 6)
+        t = time_launches(lambda: case.launch(amf_hip.DECODE_MFMA), steps, warmup)
+        log(f"{name}: {t.leg(case.algo_bytes)}")
+        return 0
+    if name in ("fp8_restore", "int4_restore", "fp8_save", "int4_save", "fp8_tensor_save"):
+        fmt = ("fp8_e4m3" if name == "fp8_tensor_save" else
+               "fp8_e4m3_ph" if name.startswith("fp8") else "int4_asym_g32")
+        case = (RestoreCase(fmt, 32, 8, 128, 16384, 2048, 3) if fmt == "int4_asym_g32"
+                else RestoreCase(fmt, 32, 8, 128, 8192, 512, 2))
+        launch = case.launch if name.endswith("restore") else case.save_launch()
+        t = time_launches(launch.launch, steps, warmup)
+        log(f"{name}: {t.leg(case.algo_bytes)}")
+        return 0
+    case = DecodeCase()
+    algo = amf_hip.DECODE_MFMA if name == "decode_mfma" else amf_hip.DECODE_VALU
+    t = time_launches(lambda: case.launch(algo), steps, warmup)
+    log(f"{name}: {t.leg(case.algo_bytes)}")
+    return 0
+
+
+PROFILES = ["fp8_restore", "int4_restore", "fp8_save", "int4_save", "fp8_tensor_save",
+            "fp8_restore_70b", "decode_70b", "decode_mfma", "decode_valu", "copy", "slot_copy",
+            "raw_gather", "raw_scatter"]
 
 
 def main() -> int:
@@ -508,10 +887,7 @@ def main() -> int:
     # 20 launches (about 6 ms of the headline kernel) bring the clocks to their
     # steady state; after 3 the first timed window still runs ~3% slower.
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--profile", choices=["fp8_restore", "int4_restore", "fp8_save", "int4_save",
-                                          "fp8_tensor_save",
-                                          "fp8_restore_70b", "decode_70b", "decode_mfma",
-                                          "decode_valu", "copy", "slot_copy"], default=None,
+    ap.add_argument("--profile", choices=PROFILES, default=None,
                     help="run only this kernel loop (for rocprofv3)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
@@ -528,61 +904,20 @@ def main() -> int:
     import amf_hip
 
     amf_hip.load()
-    torch.set_num_threads(cpu_threads())
-
+    info = host_info()
+    torch.set_num_threads(info["threads"])
     if args.profile:
-        if args.profile == "copy":
-            # Calibration for the HBM byte counters: a raw page copy of exactly
-            # 1 GiB read + 1 GiB written (2 planes of 16384 pages of 32 KiB).
-            from korith_vllm_ext import _paged
+        return run_profile(args.profile, args.steps, args.warmup)
+    want_cpu = not args.no_cpu_baseline
+    cpu_jobs = []  # (section, key, callable) run after every GPU measurement
 
-            src = torch.empty(2, 16384, 16, 8, 128, dtype=torch.bfloat16, device=DEV).fill_(1.0)
-            dst = torch.empty_like(src)
-            view = _paged.cache_view([src])
-            fn = lambda: _paged.gather_pages(view, None, [dst[0].data_ptr(), dst[1].data_ptr()],
-                                             view.page_bytes, 16384)
-            ms = time_launches(fn, args.steps, args.warmup)
-            log(f"copy: {ms:.4f} ms/launch, 1 GiB read + 1 GiB written per launch, "
-                f"{2 * 2**30 / ms / 1e6:.1f} GB/s")
-            return 0
-        if args.profile == "slot_copy":
-            cc = ConnectorCase()
-            fn, moved, keep = cc.slot_launch()
-            ms = time_launches(fn, args.steps, args.warmup)
-            log(f"slot_copy: {ms:.4f} ms/launch, {moved / ms / 1e6:.1f} GB/s")
-            return 0
-        if args.profile == "fp8_restore_70b":
-            case = RestoreCase("fp8_e4m3_ph", 80, 8, 128, 8192, 8192, 5)
-            ms = time_launches(case.launch.launch, args.steps, args.warmup)
-            log(f"{args.profile}: {ms:.4f} ms/launch, {case.algo_bytes / ms / 1e6:.1f} GB/s")
-            return 0
-        if args.profile == "decode_70b":
-            case = DecodeCase(8, 64, 8, 131072, 131072, 6)
-            ms = time_launches(lambda: case.launch(amf_hip.DECODE_MFMA), args.steps, args.warmup)
-            log(f"{args.profile}: {ms:.4f} ms/call, {case.algo_bytes / ms / 1e6:.1f} GB/s")
-            return 0
-        if args.profile in ("fp8_restore", "int4_restore", "fp8_save", "int4_save",
-                            "fp8_tensor_save"):
-            fmt = ("fp8_e4m3" if args.profile == "fp8_tensor_save" else
-                   "fp8_e4m3_ph" if args.profile.startswith("fp8") else "int4_asym_g32")
-            case = (RestoreCase(fmt, 32, 8, 128, 16384, 2048, 3) if fmt == "int4_asym_g32"
-                    else RestoreCase(fmt, 32, 8, 128, 8192, 512, 2))
-            launch = case.launch if args.profile.endswith("restore") else case.save_launch()
-            ms = time_launches(launch.launch, args.steps, args.warmup)
-            log(f"{args.profile}: {ms:.4f} ms/launch, {case.algo_bytes / ms / 1e6:.1f} GB/s")
-        else:
-            case = DecodeCase()
-            algo = amf_hip.DECODE_MFMA if args.profile == "decode_mfma" else amf_hip.DECODE_VALU
-            ms = time_launches(lambda: case.launch(algo), args.steps, args.warmup)
-            log(f"{args.profile}: {ms:.4f} ms/call, {case.algo_bytes / ms / 1e6:.1f} GB/s")
-        return 0
-
-    # ---- headline: FP8 per-(page, head) restore, Llama-3-8B shape ----
-    log("fp8 restore: building inputs")
+    # ---- headline: FP8 per-(page, head) restore, Llama-3-8B shape (C2) ----
+    log("c2 fp8 restore: building inputs")
     fp8 = RestoreCase("fp8_e4m3_ph", 32, 8, 128, 8192, 512, seed=2)
-    ms = time_launches(fp8.launch.launch, args.steps, args.warmup)
+    t = time_launches(fp8.launch.launch, args.steps, args.warmup)
+    ms = t.mean_ms
     gbs = fp8.algo_bytes / (ms * 1e-3) / 1e9
-    log(f"fp8 restore: {ms:.4f} ms, {gbs:.1f} GB/s")
+    log(f"c2 fp8 restore: mean {ms:.4f} ms, median {t.median_ms:.4f} ms, {gbs:.1f} GB/s")
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -604,72 +939,82 @@ def main() -> int:
                      "traffic": profiled_traffic("fp8_dequant_scatter_llama3_8b_512p"),
                      "kernel": "fp8_dequant_scatter_kernel",
                      "algo_bytes_per_launch": fp8.algo_bytes},
+        "host": info,
     }
-    cpu_timed = None if args.no_cpu_baseline else fp8.cpu_baseline(8)
+    c2 = {"restore": t.leg(fp8.algo_bytes)}
+    if want_cpu:
+        cpu_jobs.append(("c2_fp8_llama3_8b", "cpu_restore", fp8.cpu_baseline(8)))
     sv = fp8.save_launch()
-    ms_s = time_launches(sv.launch, args.steps, args.warmup)
-    result["fp8_save"] = {"workload": "fp8_save_llama3_8b", "ms": round(ms_s, 5),
-                          "GB/s": round(fp8.algo_bytes / ms_s / 1e6, 2),
-                          "frac": round(fp8.algo_bytes / ms_s / 1e6 / HBM_PEAK_GBS, 4)}
+    c2["save"] = time_launches(sv.launch, args.steps, args.warmup).leg(fp8.algo_bytes)
     del sv
-    log(f"fp8 save: {ms_s:.4f} ms")
-    log("fp8 restore: CompressedVRAMPool API wall clock")
-    result["pool_api"] = fp8.pool_api(args.steps, args.warmup)
-    log(f"pool api: {result['pool_api']}")
+    log(f"c2 fp8 save: {c2['save']}")
+    c2["pool_api"] = fp8.pool_api(args.steps, args.warmup)
+    log(f"c2 pool api: {c2['pool_api']}")
+    result["c2_fp8_llama3_8b"] = c2
     fp8.free()
     del fp8
 
     if not args.no_secondary:
-        log("int4 restore: building inputs")
+        # ---- C1: raw gather / scatter, Qwen2-0.5B ----
+        log("c1 raw copy: building inputs")
+        raw = RawCase()
+        c1 = {"gather": time_launches(raw.rotating(raw.gather), args.steps, args.warmup)
+              .leg(raw.algo_bytes, rotations=raw.rot),
+              "scatter": time_launches(raw.rotating(raw.scatter), args.steps, args.warmup)
+              .leg(raw.algo_bytes, rotations=raw.rot)}
+        log(f"c1 raw: {c1}")
+        if want_cpu:
+            cpu_jobs.append(("c1_raw_qwen2_0_5b", "cpu", raw.cpu_baseline()))
+        ak = AmfkCase(raw)
+        result["amfk"] = ak.run(args.steps, args.warmup)
+        ak.free()
+        log(f"amfk: {result['amfk']}")
+        result["c1_raw_qwen2_0_5b"] = c1
+        raw.free()
+        del raw, ak
+
+        # ---- C3: INT4 asym g32 ----
+        log("c3 int4 restore: building inputs")
         i4 = RestoreCase("int4_asym_g32", 32, 8, 128, 16384, 2048, seed=3)
-        ms4 = time_launches(i4.launch.launch, args.steps, args.warmup)
-        g4 = i4.algo_bytes / (ms4 * 1e-3) / 1e9
-        log(f"int4 restore: {ms4:.4f} ms, {g4:.1f} GB/s")
-        result["int4_restore"] = {"workload": "int4_restore_llama3_8b", "ms": round(ms4, 5),
-                                  "GB/s": round(g4, 2), "frac": round(g4 / HBM_PEAK_GBS, 4),
-                                  "algo_bytes": i4.algo_bytes}
+        c3 = {"restore": time_launches(i4.launch.launch, args.steps, args.warmup)
+              .leg(i4.algo_bytes)}
+        if want_cpu:
+            cpu_jobs.append(("c3_int4_llama3_8b", "cpu_restore", i4.cpu_baseline(2, 3, 2.0)))
         sv4 = i4.save_launch()
-        ms4s = time_launches(sv4.launch, args.steps, args.warmup)
-        result["int4_save"] = {"workload": "int4_save_llama3_8b", "ms": round(ms4s, 5),
-                               "GB/s": round(i4.algo_bytes / ms4s / 1e6, 2),
-                               "frac": round(i4.algo_bytes / ms4s / 1e6 / HBM_PEAK_GBS, 4)}
+        c3["save"] = time_launches(sv4.launch, args.steps, args.warmup).leg(i4.algo_bytes)
         del sv4
-        log(f"int4 save: {ms4s:.4f} ms")
+        log(f"c3 int4: {c3}")
+        result["c3_int4_llama3_8b"] = c3
         i4.free()
         del i4
 
-        log("int4 decode: building inputs")
+        # ---- C4: INT4 paged decode ----
+        log("c4 int4 decode: building inputs")
         dc = DecodeCase()
-        res = {}
-        for name, algo in (("mfma", amf_hip.DECODE_MFMA), ("valu", amf_hip.DECODE_VALU)):
-            msd = time_launches(lambda: dc.launch(algo), args.steps, args.warmup)
-            res[name] = msd
-        msd = res["mfma"]
-        gd = dc.algo_bytes / (msd * 1e-3) / 1e9
-        result["int4_decode"] = {
-            "workload": "decode_llama3_8b", "batch": dc.batch, "sum_ctx": dc.sum_ctx,
-            "ms_per_layer_call": round(msd, 5),
-            "tok_per_s_per_layer": round(dc.batch / (msd * 1e-3), 1),
-            "tok_per_s_model_32_layers": round(dc.batch / (32 * msd * 1e-3), 1),
-            "kv_tok_per_s": round(dc.sum_ctx / (msd * 1e-3), 1),
-            "GB/s": round(gd, 2), "frac": round(gd / HBM_PEAK_GBS, 4),
-            "valu_ms": round(res["valu"], 5), "mfma_over_valu_speedup": round(res["valu"] / msd, 3),
-        }
-        log(f"int4 decode: mfma {msd:.4f} ms ({gd:.1f} GB/s), valu {res['valu']:.4f} ms")
+        tv = time_launches(lambda: dc.launch(amf_hip.DECODE_VALU), args.steps, args.warmup)
+        td = time_launches(lambda: dc.launch(amf_hip.DECODE_MFMA), args.steps, args.warmup)
+        msd = td.median_ms
+        result["c4_decode_llama3_8b"] = {"decode": td.leg(
+            dc.algo_bytes, workload="decode_llama3_8b", batch=dc.batch, sum_ctx=dc.sum_ctx,
+            tok_per_s_per_layer=round(dc.batch / (msd * 1e-3), 1),
+            tok_per_s_model_32_layers=round(dc.batch / (32 * msd * 1e-3), 1),
+            kv_tok_per_s=round(dc.sum_ctx / (msd * 1e-3), 1),
+            valu_median_ms=round(tv.median_ms, 5),
+            mfma_over_valu_speedup=round(tv.median_ms / msd, 3))}
+        log(f"c4 decode: {result['c4_decode_llama3_8b']}")
+        if want_cpu:
+            cpu_jobs.append(("c4_decode_llama3_8b", "cpu_fallback", dc.cpu_fallback(4)))
         del dc
         torch.cuda.empty_cache()
+
         log("reference formats: restore and save at the Llama-3-8B shape")
         fmts = {}
         for fmt in ("fp8_e4m3", "int4_sym_block", "int4_sym"):
             rc = RestoreCase(fmt, 32, 8, 128, 8192, 512, seed=8)
-            r_ms = time_launches(rc.launch.launch, args.steps, args.warmup)
+            r = time_launches(rc.launch.launch, args.steps, args.warmup).leg(rc.algo_bytes)
             sv = rc.save_launch()
-            s_ms = time_launches(sv.launch, args.steps, args.warmup)
-            fmts[fmt] = {"restore_ms": round(r_ms, 5),
-                         "restore_GB/s": round(rc.algo_bytes / r_ms / 1e6, 1),
-                         "save_ms": round(s_ms, 5),
-                         "save_GB/s": round(rc.algo_bytes / s_ms / 1e6, 1),
-                         "algo_bytes": rc.algo_bytes}
+            s_ = time_launches(sv.launch, args.steps, args.warmup).leg(rc.algo_bytes)
+            fmts[fmt] = {"restore": r, "save": s_}
             del sv
             rc.free()
         result["reference_formats_llama3_8b_512p"] = fmts
@@ -680,15 +1025,21 @@ def main() -> int:
         log(f"connector: {result['connector']}")
         cc.free()
         del cc
-        result.update(long_context_70b(args.steps, args.warmup))
-    if cpu_timed is not None:
-        log("fp8 restore: CPU baseline (8 of 32 layers, >= 10 s)")
-        cb = cpu_timed()
-        result["cpu_baseline"] = {"value": round(cb["value"], 3), "unit": "GB/s",
-                                  "cores": torch.get_num_threads(), "kind": "port",
-                                  "sample": cb["sample"], "seconds": round(cb["seconds"], 3),
-                                  "cpu": platform.processor() or platform.machine(),
-                                  "torch": torch.__version__}
+        result["c5_llama3_70b"] = long_context_70b(args.steps, args.warmup, cpu_jobs, want_cpu)
+
+    for section, key, job in cpu_jobs:
+        log(f"cpu baseline: {section} {key}")
+        res = job()
+        res.update({"cores": info["threads"], "kind": "port"})
+        result.setdefault(section, {})[key] = res
+        log(f"cpu baseline: {section} {key}: {res}")
+    head = result.get("c2_fp8_llama3_8b", {}).get("cpu_restore")
+    if head is not None:
+        result["cpu_baseline"] = {"value": head["GB/s"], "unit": "GB/s",
+                                  "cores": info["threads"], "kind": "port",
+                                  "sample": head["sample"], "seconds": head["seconds"],
+                                  "cpu": info["cpu"], "torch": info["torch"],
+                                  "parity_vs_gpu": head["parity_vs_gpu"]}
     print(json.dumps(result), flush=True)
     return 0
 

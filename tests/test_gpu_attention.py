@@ -121,6 +121,50 @@ def test_paged_contract_int4_pool(R):
     assert err <= 2e-2, err
 
 
+def test_paged_contract_caller_buffers():
+    """The keyword path with caller-owned `out` and `workspace`: correct
+    buffers are used as given (same result as without them); a buffer on the
+    CPU, non-contiguous, of the wrong shape or dtype is refused with
+    ValueError before any launch (the output stays untouched)."""
+    import amf_hip
+    from korith_vllm_ext.codecs import get_codec
+    from korith_vllm_ext.int4_decode_attention import int4_decode_attention
+
+    g = torch.Generator().manual_seed(123)
+    Hkv, R, D, pool = 2, 4, 128, 40
+    pages = gen.kv_values((2, pool, 16, Hkv, D), D, g, True)
+    ckv = get_codec("int4_asym_g32").compress(pages.to(DEV))
+    ctx = torch.tensor([100, 333, 5], dtype=torch.int32, device=DEV)
+    bt = torch.stack([torch.randperm(pool, generator=g)[:21] for _ in range(3)]).to(torch.int32)
+    bt = bt.to(DEV)
+    q = torch.randn(3, Hkv * R, D, generator=g).to(torch.bfloat16).to(DEV)
+    want = int4_decode_attention(q, ckv, block_tables=bt, context_lens=ctx,
+                                 out_dtype=torch.float32)
+    wsb = amf_hip.decode_workspace_bytes(3, Hkv * R, Hkv, D, 21 * 16)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    out = torch.full((3, Hkv * R, D), 9.0, dtype=torch.float32, device=DEV)
+    got = int4_decode_attention(q, ckv, block_tables=bt, context_lens=ctx, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    assert got.data_ptr() == out.data_ptr() and torch.equal(got, want)
+    sentinel = torch.full_like(out, 9.0)
+    bad = [
+        dict(out=torch.empty(3, Hkv * R, D)),                                      # on the CPU
+        dict(out=torch.empty(3, D, Hkv * R, device=DEV).transpose(1, 2)),          # strided
+        dict(out=torch.empty(3, Hkv * R, D + 8, device=DEV)),                      # shape
+        dict(out=sentinel.clone(), out_dtype=torch.float16),                       # dtype
+        dict(out=sentinel.clone(), workspace=torch.empty(wsb, dtype=torch.uint8)),  # ws on CPU
+        dict(out=sentinel.clone(),
+             workspace=torch.empty(2 * wsb, dtype=torch.uint8, device=DEV)[::2]),  # strided ws
+    ]
+    for kw in bad:
+        with pytest.raises(ValueError):
+            int4_decode_attention(q, ckv, block_tables=bt, context_lens=ctx, **kw)
+        o = kw["out"]
+        if o.is_cuda and o.is_contiguous() and o.shape == sentinel.shape:
+            torch.cuda.synchronize()
+            assert torch.equal(o, sentinel)
+
+
 def test_dispatch_resolves_to_hip_kernel():
     from korith_vllm_ext.kernels import dispatch
 

@@ -416,6 +416,13 @@ def test_connector_flat_caches_and_misses():
         f"model.layers.{l}.attn": SimpleNamespace(kv_cache=again[l]) for l in range(L)}))
     torch.cuda.synchronize()
     assert all(torch.count_nonzero(t).item() == 0 for t in again)
+    # the missed load's blocks go back to vLLM for recomputation (once), and
+    # the scheduler no longer reports the evicted prefix as a hit
+    n_valid = paging.align_to_block_size(len(prompt), 16) // 16
+    assert c.get_block_ids_with_load_errors() == set(warm_blocks[:n_valid])
+    assert c.get_block_ids_with_load_errors() == set()
+    assert req.prefix_hash not in c._known_hashes
+    assert c.get_num_new_matched_tokens(SimpleNamespace(prompt_token_ids=prompt), 0) == (0, False)
 
 
 @pytest.mark.parametrize("fmt,bs", [("fp8_e4m3_ph", 32), ("int4_asym_g32", 64),

@@ -172,6 +172,33 @@ def test_vllm_roundtrip_bitexact(fmt, dtype):
     assert p.restore_to_vllm("nope", target, dst) == 0
 
 
+def test_failed_per_tensor_fp8_save_is_a_miss():
+    """A per-tensor FP8 save whose layer absmax comes back non-finite (what
+    the single-read kernel writes for a scale group whose wait gave up) is
+    dropped on first lookup: get() misses, restore_to_vllm restores nothing
+    and returns 0, and the entry's spans are free again."""
+    L, pool_pages, n, H, D = 2, 32, 8, 2, 64
+    g = torch.Generator().manual_seed(17)
+    cache = [gen.kv_values((2, pool_pages, 16, H, D), D, g, True).to(DEV) for _ in range(L)]
+    p = _pool(num_layers=L, bytes_per_layer=1 << 20, block_bytes=1 << 12,
+              default_format="fp8_e4m3")
+    assert p.put_from_vllm("bad", cache, list(range(n)), n * 16)
+    host, ev = p._index["bad"].pending_absmax
+    ev.synchronize()
+    host.view(torch.float32)[1] = float("inf")   # layer 1's save "gave up"
+    target = sentinel_cache(L, pool_pages, 16, H, D, torch.bfloat16, DEV)
+    before = p.stats()["misses"]
+    assert p.restore_to_vllm("bad", target, list(range(n))) == 0
+    assert p.get("bad") is None and "bad" not in p
+    assert p.stats()["misses"] == before + 2
+    assert all(a.free_blocks() == a.n_blocks for a in p._alloc)
+    torch.cuda.synchronize()
+    assert all(bool((t == -7.25).all()) for t in target)
+    # a good save of the same key afterwards is a normal hit
+    assert p.put_from_vllm("bad", cache, list(range(n)), n * 16)
+    assert p.restore_to_vllm("bad", target, list(range(n))) == n * 16
+
+
 def test_vllm_one_byte_cache_is_stored_raw():
     L, pool_pages, n = 2, 16, 6
     cache = [torch.randint(0, 256, (2, pool_pages, 16, 2, 64), dtype=torch.uint8, device=DEV)
