@@ -114,6 +114,11 @@ SIGNATURES = {
          _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_ptr, _c_i64, _c_i32, _c_ptr,
          _c_ptr],
     ),
+    "amf_int4_paged_decode_attn_noalloc": (
+        _c_i32,
+        [_c_ptr, _c_i32, _c_ptr, _c_i32, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i32,
+         _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_ptr, _c_ptr],
+    ),
     "amf_fnv1a64": (ctypes.c_uint64, [_c_ptr, _c_i64, ctypes.c_uint64]),
     "amf_hash_tokens": (ctypes.c_uint64, [_c_ptr, _c_i64]),
     "amf_dense_attn": (

@@ -35,6 +35,8 @@
 //        the row of each output column's own group is used.
 // VALU path: the same data flow with fp32 FMAs (kept for the MFMA-vs-VALU
 // comparison and as a second implementation).
+#include <mutex>
+
 #include "amf_internal.h"
 #include "amf_kernel_util.h"
 
@@ -858,6 +860,46 @@ int choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context_len
   return (int)split;
 }
 
+// ---- scratch for the entry point that allocates nothing -----------------------
+// One array per device that loads the library, held until the process ends.
+// Host code never passes `scratch` itself to a kernel (in host code the name is
+// a stand-in, not a device address): scratch_address() asks the runtime for
+// the current device's copy once and keeps it.
+constexpr int64_t kDecodeScratchBytes = 64ll << 20;
+static __device__ __align__(256) uint8_t scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Address of the current device's scratch (looked up on the first call on
+// that device, with it current), or nullptr with the error recorded.
+void* scratch_address(const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(AMF_ERR_RUNTIME, "%s: hipGetDevice failed: %s", who, hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(AMF_ERR_UNSUPPORTED, "%s: device %d beyond the %d this library tracks", who, dev,
+         kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(AMF_ERR_RUNTIME, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+           hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 extern "C" int64_t amf_int4_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
@@ -970,4 +1012,28 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
   else
     int4_decode_merge_kernel<AMF_DTYPE_F32><<<mgrid, kMergeThreads, 0, st>>>(a);
   return check_launch(who);
+}
+
+extern "C" int amf_int4_paged_decode_attn_noalloc(
+    const void* q, int32_t q_dtype, void* out, int32_t out_dtype, const void* k_codes,
+    const void* k_params, const void* v_codes, const void* v_params, int64_t pool_pages,
+    const int32_t* block_tables, int32_t block_table_stride, const int32_t* context_lens,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t max_context_len, float softmax_scale, int32_t algo,
+    int32_t* err_flag, void* stream) {
+  const char* who = "amf_int4_paged_decode_attn_noalloc";
+  const int64_t need = amf_int4_decode_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
+                                                       head_dim, max_context_len);
+  if (need > kDecodeScratchBytes)
+    return fail(AMF_ERR_WORKSPACE,
+                "%s: %lld bytes of split partials exceed the %lld-byte scratch (use "
+                "amf_int4_paged_decode_attn with a workspace)",
+                who, (long long)need, (long long)kDecodeScratchBytes);
+  void* ws = scratch_address(who);
+  if (!ws) return AMF_ERR_RUNTIME;
+  return amf_int4_paged_decode_attn(q, q_dtype, out, out_dtype, k_codes, k_params, v_codes,
+                                    v_params, pool_pages, block_tables, block_table_stride,
+                                    context_lens, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                    block_size, max_context_len, softmax_scale, ws,
+                                    kDecodeScratchBytes, algo, err_flag, stream);
 }

@@ -284,6 +284,28 @@ int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* out, int32_
                                void* workspace, int64_t workspace_bytes,
                                int32_t algo, int32_t* err_flag, void* stream);
 
+/* amf_int4_paged_decode_attn without the workspace arguments: the split
+ * partials go to a scratch array inside the library (one 64 MiB array per GPU
+ * that loads the library, held until the process ends), so the call makes no
+ * device allocation of its own or through the caller.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc).  A call whose
+ * partials (amf_int4_decode_workspace_bytes()) exceed 64 MiB returns
+ * AMF_ERR_WORKSPACE before any launch.  Every call on a GPU shares that GPU's
+ * array and it keeps the last call's contents: calls that overlap on one GPU
+ * (different streams, or threads without ordering) race; order them on one
+ * stream.  Arguments and results otherwise as amf_int4_paged_decode_attn. */
+int amf_int4_paged_decode_attn_noalloc(const void* q, int32_t q_dtype, void* out,
+                                       int32_t out_dtype, const void* k_codes,
+                                       const void* k_params, const void* v_codes,
+                                       const void* v_params, int64_t pool_pages,
+                                       const int32_t* block_tables, int32_t block_table_stride,
+                                       const int32_t* context_lens, int32_t num_seqs,
+                                       int32_t num_q_heads, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t block_size,
+                                       int32_t max_context_len, float softmax_scale,
+                                       int32_t algo, int32_t* err_flag, void* stream);
+
 /* ---- prefix keys (host functions, no device work) ---------------------------
  * FNV-1a over bytes, continuing from hash h (pass AMF_FNV_OFFSET to start).
  * Replaces _fnv1a_bytes (amf_kv_manager.py:69-72; C++ hash_bytes of
