@@ -286,7 +286,7 @@ def address_table(addrs: Sequence[int], device):
     import torch
 
     dev = torch.device(device)
-    key = (dev.type, dev.index, tuple(int(a) for a in addrs))
+    key = (dev.type, dev.index, tuple(map(int, addrs)))
     sid = stream_handle(dev)
     with _lock:
         hit = _TABLES.get(key)

@@ -19,10 +19,13 @@ include/amf_hip.h.
 from __future__ import annotations
 
 import math
+import weakref
+from collections import OrderedDict
 from dataclasses import dataclass, field
 from functools import cached_property
 from typing import List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 import amf_hip
@@ -222,7 +225,34 @@ def _kv_planes(layer: torch.Tensor):
     )
 
 
+# Geometry of recently seen cache lists, by the identity of their tensors
+# (weak references: a cached entry never keeps a cache alive, and a freed
+# tensor whose id is reused fails the identity check).  A view only reads
+# shapes, strides and addresses, which a live tensor object keeps (vLLM
+# allocates its KV caches once), so a hit skips the per-layer attribute reads.
+_VIEWS: "OrderedDict[tuple, tuple]" = OrderedDict()
+_VIEWS_MAX = 64
+
+
 def cache_view(gpu_cache: Sequence[torch.Tensor]) -> CacheView:
+    key = tuple(map(id, gpu_cache))
+    hit = _VIEWS.get(key)
+    if hit is not None:
+        refs, v = hit
+        if all(r() is t for r, t in zip(refs, gpu_cache)):
+            _VIEWS.move_to_end(key)
+            return CacheView(v.planes, v.page_stride, v.pool_pages, v.block_size, v.num_heads,
+                             v.head_dim, v.dtype, v.device, keep=list(gpu_cache))
+    view = _make_cache_view(gpu_cache)
+    geom = CacheView(view.planes, view.page_stride, view.pool_pages, view.block_size,
+                     view.num_heads, view.head_dim, view.dtype, view.device, keep=[])
+    _VIEWS[key] = ([weakref.ref(t) for t in gpu_cache], geom)
+    while len(_VIEWS) > _VIEWS_MAX:
+        _VIEWS.popitem(last=False)
+    return view
+
+
+def _make_cache_view(gpu_cache: Sequence[torch.Tensor]) -> CacheView:
     if len(gpu_cache) == 0:
         raise ValueError("empty KV cache")
     planes: List[int] = []
@@ -293,6 +323,8 @@ def _device_ids(ids, device) -> Optional[torch.Tensor]:
     if ids is None:
         return None
     if isinstance(ids, torch.Tensor) and ids.device.type != "cpu":
+        if ids.dtype == torch.int32 and ids.device == torch.device(device) and ids.is_contiguous():
+            return ids
         return ids.to(device=device, dtype=torch.int32).contiguous()
     if isinstance(ids, torch.Tensor):
         host = ids.to(torch.int32).contiguous()
@@ -357,11 +389,10 @@ def blob_tables(layout: BlobLayout, blob_bases: Sequence[int], planes_per_blob: 
                 device) -> PlaneTables:
     """Code/param plane tables for blobs at `blob_bases` (one blob per group of
     planes_per_blob planes)."""
-    codes, params = [], []
-    for base in blob_bases:
-        for p in range(planes_per_blob):
-            codes.append(base + layout.code_offset(p))
-            params.append(base + layout.param_offset(p))
+    co = [layout.code_offset(p) for p in range(planes_per_blob)]
+    po = [layout.param_offset(p) for p in range(planes_per_blob)]
+    codes = [base + o for base in blob_bases for o in co]
+    params = [base + o for base in blob_bases for o in po]
     return PlaneTables(amf_hip.address_table(codes, device), amf_hip.address_table(params, device))
 
 
@@ -488,6 +519,7 @@ class SlotMap:
         else:
             host = torch.tensor(list(slots), dtype=torch.int64)
         self.host = host.contiguous()
+        self._np = self.host.numpy()  # shares the tensor's memory
         self.n = int(self.host.numel())
         self._dev = {}
         self._checked = set()
@@ -521,8 +553,8 @@ class SlotMap:
         n = self.n if n is None else n
         if (pool_slots, n) in self._checked:
             return
-        a = self.host[:n]
-        if a.numel() and (int(a.min()) < 0 or int(a.max()) >= pool_slots):
+        a = self._np[:n]
+        if a.size and (int(a.min()) < 0 or int(a.max()) >= pool_slots):
             raise ValueError(f"slot id out of range [0, {pool_slots}): min {int(a.min())} "
                              f"max {int(a.max())}")
         self._checked.add((pool_slots, n))
@@ -530,31 +562,37 @@ class SlotMap:
     def page_ids(self, n_tokens: int, block_size: int) -> Optional[List[int]]:
         """Block ids when the first n_tokens slots are whole pages in order
         (token p*block_size + i at slot b_p*block_size + i); None otherwise."""
+        ids = self._page_array(n_tokens, block_size)
+        return None if ids is None else ids.tolist()
+
+    def _page_array(self, n_tokens: int, block_size: int) -> Optional[np.ndarray]:
         key = (n_tokens, block_size)
         if key not in self._pages:
             self._pages[key] = self._page_ids(n_tokens, block_size)
         return self._pages[key]
 
-    def _page_ids(self, n_tokens: int, block_size: int) -> Optional[List[int]]:
+    def _page_ids(self, n_tokens: int, block_size: int) -> Optional[np.ndarray]:
         if n_tokens <= 0 or n_tokens > self.n or n_tokens % block_size:
             return None
-        a = self.host[:n_tokens].view(-1, block_size)
+        a = self._np[:n_tokens].reshape(-1, block_size)
         first = a[:, 0]
-        if bool((first % block_size != 0).any()):
+        if (first % block_size).any():
             return None
-        if not torch.equal(a, first[:, None] + torch.arange(block_size, dtype=torch.int64)):
+        if not np.array_equal(a, first[:, None] + np.arange(block_size, dtype=np.int64)):
             return None
-        return (first // block_size).tolist()
+        ids = first // block_size
+        if ids.size and int(ids.max()) > np.iinfo(np.int32).max:
+            return None
+        return ids.astype(np.int32)
 
     def page_ids_on(self, n_tokens: int, block_size: int, device) -> Optional[torch.Tensor]:
         """page_ids as a device int32 tensor, made once per device."""
-        ids = self.page_ids(n_tokens, block_size)
+        ids = self._page_array(n_tokens, block_size)
         if ids is None:
             return None
         dev = torch.device(device)
         return self._cached_on((dev.type, dev.index, n_tokens, block_size), dev,
-                               lambda: amf_hip.to_device(torch.tensor(ids, dtype=torch.int32),
-                                                         dev))
+                               lambda: amf_hip.to_device(torch.from_numpy(ids), dev))
 
 
 def _row_bytes(view: CacheView) -> int:

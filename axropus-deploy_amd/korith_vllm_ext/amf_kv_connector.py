@@ -49,6 +49,7 @@ from __future__ import annotations
 import enum
 import hashlib
 import logging
+import weakref
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Any, Dict, List, Optional, Tuple
 
@@ -163,22 +164,25 @@ def _layer_index(layer_name: str) -> Optional[int]:
 
 
 def _layer_groups(layers: List[Tuple[int, str, torch.Tensor]]) -> List[list]:
-    """Split index-sorted (index, name, cache) layers into launch groups of
-    1, 1, 2, 4, 8, ... consecutive layers of one geometry: the first layers
-    are ready after a short launch, the later ones, needed later, come in
-    larger launches with less host work per layer."""
+    """Split index-sorted (index, name, cache) layers into launch groups: the
+    first layer alone (the forward's first attention waits only for a short
+    launch), then runs of consecutive layers of one geometry in one launch
+    each.  A launch costs tens of microseconds of host work, more than the
+    device time of a few layers, so the rest are not cut further: by the
+    time the forward reaches the second layer the one large launch is well
+    under way."""
     groups: List[list] = []
-    cap = 1
+    geom_prev = None
     for item in layers:
+        t = item[2]
+        geom = (t.shape, t.stride(), t.dtype)
         g = groups[-1] if groups else None
-        if (g is not None and len(g) < cap and item[0] == g[-1][0] + 1
-                and item[2].shape == g[-1][2].shape and item[2].stride() == g[-1][2].stride()
-                and item[2].dtype == g[-1][2].dtype):
+        if (g is not None and len(groups) > 1 and item[0] == g[-1][0] + 1
+                and geom == geom_prev):
             g.append(item)
-            continue
-        if g is not None:
-            cap = len(groups[-1]) * 2 if len(groups) > 1 else 1
-        groups.append([item])
+        else:
+            groups.append([item])
+        geom_prev = geom
     return groups
 
 
@@ -257,6 +261,9 @@ class AMFKVConnector(KVConnectorBase_V1):
         self._load_stream: Optional[torch.cuda.Stream] = None
         self._layer_events: Dict[str, torch.cuda.Event] = {}
         self._waited: set = set()  # (event, stream) pairs already waited this step
+        self._last_load_event: Optional[torch.cuda.Event] = None  # the step's final restore
+        self._device_index = 0
+        self._groups_memo = None
 
         logger.info(
             "[AMF_CONNECTOR] init role=%s layers=%d heads=%d head_dim=%d bytes_per_layer=%d "
@@ -378,6 +385,40 @@ class AMFKVConnector(KVConnectorBase_V1):
             return kv.view(2, kv.shape[1], 1, self._num_kv_heads, self._head_dim)
         return None
 
+    def _load_groups(self, forward_context: Any) -> List[list]:
+        """The step's attention layers as launch groups of (index, name, paged
+        cache), rebuilt only when the layers' cache tensors change (vLLM
+        passes the same tensors every step; the memo holds weak references)."""
+        ve = getattr(forward_context, "virtual_engine", 0) or 0
+        items = []
+        for name, layer in forward_context.no_compile_layers.items():
+            kv = getattr(layer, "kv_cache", None)
+            if isinstance(kv, (list, tuple)):
+                kv = kv[ve] if len(kv) > ve else None
+            items.append((name, kv))
+        key = tuple((name, id(kv)) for name, kv in items)
+        memo = self._groups_memo
+        if memo is not None and memo[0] == key and all(
+                r() is kv for r, (_, kv) in zip(memo[1], items)):
+            return memo[2]
+        layers = []
+        for name, kv in items:
+            idx = self._layer_name_to_idx(name)
+            if kv is None or idx is None or not isinstance(kv, torch.Tensor) or kv.numel() == 0:
+                continue
+            pk = self._paged_layer(kv)
+            if pk is None:
+                logger.warning("[AMF_CONNECTOR] Unexpected kv_cache shape %s for %s",
+                               tuple(kv.shape), name)
+                continue
+            layers.append((idx, name, pk))
+        layers.sort(key=lambda t: t[0])
+        groups = _layer_groups(layers)
+        refs = [weakref.ref(kv) if isinstance(kv, torch.Tensor) else (lambda: None)
+                for _, kv in items]
+        self._groups_memo = (key, refs, groups)
+        return groups
+
     def start_load_kv(self, forward_context: Any, **kwargs: Any) -> None:
         """Restore every hit request of this step into its slots, in layer
         groups, on the load stream (reference: :326-392, which restores
@@ -412,21 +453,13 @@ class AMFKVConnector(KVConnectorBase_V1):
         if not hits:
             return
 
-        ve = getattr(forward_context, "virtual_engine", 0) or 0
-        layers = []
-        for name, layer in forward_context.no_compile_layers.items():
-            kv = getattr(layer, "kv_cache", None)
-            if isinstance(kv, (list, tuple)):
-                kv = kv[ve] if len(kv) > ve else None
-            idx = self._layer_name_to_idx(name)
-            if kv is None or idx is None or not isinstance(kv, torch.Tensor) or kv.numel() == 0:
-                continue
-            layers.append((idx, name, kv))
-        layers.sort(key=lambda t: t[0])
-        if not layers:
+        groups = self._load_groups(forward_context)
+        if not groups:
             return
 
         device = pool.device
+        self._device_index = device.index if device.index is not None else \
+            torch.cuda.current_device()
         forward = torch.cuda.current_stream(device)
         stream = forward
         if self._side_load:
@@ -434,16 +467,8 @@ class AMFKVConnector(KVConnectorBase_V1):
                 self._load_stream = torch.cuda.Stream(device)  # default priority
             stream = self._load_stream
             stream.wait_stream(forward)
-        paged = []
-        for idx, name, kv in layers:
-            pk = self._paged_layer(kv)
-            if pk is None:
-                logger.warning("[AMF_CONNECTOR] Unexpected kv_cache shape %s for %s",
-                               tuple(kv.shape), name)
-                continue
-            paged.append((idx, name, pk))
         with torch.cuda.stream(stream):
-            for group in _layer_groups(paged):
+            for group in groups:
                 first = group[0][0]
                 caches = [pk for _, _, pk in group]
                 for req, entry, slots in hits:
@@ -454,6 +479,7 @@ class AMFKVConnector(KVConnectorBase_V1):
                     ev.record(stream)
                     for _, name, _ in group:
                         self._layer_events[name] = ev
+                    self._last_load_event = ev
         for req, _, _ in hits:
             logger.info("[AMF_CONNECTOR] Loaded prefix=%s into paged buffer",
                         req.prefix_hash[:12])
@@ -464,7 +490,7 @@ class AMFKVConnector(KVConnectorBase_V1):
         ev = self._layer_events.pop(layer_name, None)
         if ev is None:
             return
-        key = (id(ev), amf_hip.stream_handle(self._pool.device))
+        key = (id(ev), torch._C._cuda_getCurrentRawStream(self._device_index))
         if key not in self._waited:  # layers of one launch share its event
             self._waited.add(key)
             torch.cuda.current_stream(self._pool.device).wait_event(ev)
@@ -496,10 +522,15 @@ class AMFKVConnector(KVConnectorBase_V1):
         """Store each noted prefix, layers in index order, in the pool's
         default format (reference: :438-483)."""
         pool = self._ensure_pool()
-        if pool is not None and self._load_stream is not None:
+        ev, self._last_load_event = self._last_load_event, None
+        if pool is not None and ev is not None:
             # every restore of the step is ordered before the next step's work,
-            # also for a layer whose wait_for_layer_load never came
-            torch.cuda.current_stream(pool.device).wait_stream(self._load_stream)
+            # also for a layer whose wait_for_layer_load never came (the last
+            # layer's wait usually did this already)
+            key = (id(ev), torch._C._cuda_getCurrentRawStream(self._device_index))
+            if key not in self._waited:
+                self._waited.add(key)
+                torch.cuda.current_stream(pool.device).wait_event(ev)
         self._save_slots.clear()
         if pool is None or not self._save_layers:
             self._save_layers.clear()

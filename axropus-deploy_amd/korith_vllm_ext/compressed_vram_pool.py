@@ -116,6 +116,9 @@ class PoolEntry:
     cache_dtype: Optional[torch.dtype] = None
     # last launch that touched the entry's spans, per stream (stream id -> event)
     fences: Dict[int, torch.cuda.Event] = field(default_factory=dict)
+    # per stream id, the fence events that stream has already been ordered
+    # after (held, so a later fence is never mistaken for one of them)
+    waited: Dict[int, List[torch.cuda.Event]] = field(default_factory=dict)
     pending_absmax: Optional[Tuple[torch.Tensor, torch.cuda.Event]] = None
 
     def nbytes(self) -> int:
@@ -192,7 +195,7 @@ class _SlabAllocator:
         return None
 
     def free(self, start: int, n: int, fences: Sequence = ()) -> None:
-        fences = [f for f in fences if f is not None]
+        fences = _prune(fences) if fences else []
         i = 0
         while i < len(self._runs) and self._runs[i][0] < start:
             i += 1
@@ -223,15 +226,21 @@ class _SlabAllocator:
         self._runs = [[used_prefix, n, fences]] if n > 0 else []
 
 
+_PRUNE_QUERY_AT = 8  # fences a run may hold before completed ones are queried out
+
+
 def _prune(fences: list) -> list:
-    """Drop events that have completed (non-blocking query) and duplicates."""
+    """Drop duplicates, and once the list is long, events that have completed
+    (non-blocking query).  Waiting on a completed event costs nothing, while
+    a query is a runtime call per event: short lists are kept as they are."""
     out, seen = [], set()
     for e in fences:
         if e is None or id(e) in seen:
             continue
         seen.add(id(e))
-        if not e.query():
-            out.append(e)
+        out.append(e)
+    if len(out) >= _PRUNE_QUERY_AT:
+        out = [e for e in out if not e.query()]
     return out
 
 
@@ -291,6 +300,8 @@ class CompressedVRAMPool:
             torch.empty(self._blocks_per_layer * block_bytes, dtype=torch.uint8, device=device)
             for _ in range(num_layers)
         ]
+        # slab base addresses (slabs never move), read on every launch
+        self._slab_ptr: List[int] = [t.data_ptr() for t in self._slabs]
         self._alloc = [_SlabAllocator(self._blocks_per_layer) for _ in range(num_layers)]
 
         self._index: Dict[str, PoolEntry] = {}
@@ -403,7 +414,7 @@ class CompressedVRAMPool:
                 if entry.format == FMT_RAW and view.dtype.itemsize != lay.elem_bytes:
                     raise ValueError(f"raw entry of {lay.elem_bytes}-byte elements cannot fill a "
                                      f"{view.dtype} cache")
-                bases = [self._slabs[b.layer_id].data_ptr() + b.data_offset
+                bases = [self._slab_ptr[b.layer_id] + b.data_offset
                          for b in entry.blocks[:layers]]
                 self._wait(entry)
                 if entry.format == FMT_RAW:
@@ -483,7 +494,7 @@ class CompressedVRAMPool:
         with self._lock:
             lay = entry.layout
             L = entry.num_layers
-            bases = [self._slabs[b.layer_id].data_ptr() + b.data_offset for b in entry.blocks]
+            bases = [self._slab_ptr[b.layer_id] + b.data_offset for b in entry.blocks]
             shape = tuple(entry.blobs[0].shape)
             T = entry.blobs[0].meta["n_tokens"]
             self._wait(entry)
@@ -590,7 +601,7 @@ class CompressedVRAMPool:
             if n == 0:
                 return 0
             slots.check(view.pool_pages * view.block_size, n)
-            bases = [self._slabs[b.layer_id].data_ptr() + b.data_offset
+            bases = [self._slab_ptr[b.layer_id] + b.data_offset
                      for b in entry.blocks[first_layer:first_layer + layers]]
             P = lay.block_size
             row = H * D * view.dtype.itemsize
@@ -665,10 +676,15 @@ class CompressedVRAMPool:
                 logger.warning("CompressedVRAMPool: no room for %s (%d x %d slab blocks, %s)",
                                prefix_hash[:12], L, need, fmt)
                 return False
-            for fences in (f for _, f in spans):
+            # the layers' spans mostly carry the same events: wait once each
+            stream = torch.cuda.current_stream(self.device)
+            seen = set()
+            for _, fences in spans:
                 for ev in fences:
-                    torch.cuda.current_stream(self.device).wait_event(ev)
-            bases = [self._slabs[l].data_ptr() + start * self.block_bytes
+                    if id(ev) not in seen:
+                        seen.add(id(ev))
+                        stream.wait_event(ev)
+            bases = [self._slab_ptr[l] + start * self.block_bytes
                      for l, (start, _) in enumerate(spans)]
             pending = None
             if fmt == FMT_RAW:
@@ -774,11 +790,14 @@ class CompressedVRAMPool:
         """Order this stream after the entry's launches on other streams (its
         save may have run elsewhere)."""
         sid = amf_hip.stream_handle(self.device)
-        others = [ev for s, ev in entry.fences.items() if s != sid]
+        done = entry.waited.get(sid, ())
+        others = [ev for s, ev in entry.fences.items()
+                  if s != sid and not any(ev is d for d in done)]
         if others:
             stream = torch.cuda.current_stream(self.device)
             for ev in others:
                 stream.wait_event(ev)
+            entry.waited[sid] = [ev for s, ev in entry.fences.items() if s != sid]
 
     def _allocate(self, L: int, need: int) -> Optional[List[Tuple[int, list]]]:
         """One span of `need` slab blocks on each of the first L layers,
@@ -819,8 +838,9 @@ class CompressedVRAMPool:
         return True
 
     def _release_entry(self, entry: PoolEntry) -> None:
+        fences = _prune(list(entry.fences.values()))
         for b in entry.blocks:
-            self._alloc[b.layer_id].free(b.block_id, b.span_blocks, list(entry.fences.values()))
+            self._alloc[b.layer_id].free(b.block_id, b.span_blocks, fences)
 
     def _allocate_with_compaction(self, L: int, need: int):
         """Allocation with slab compaction as the last resort (reference:

@@ -162,7 +162,7 @@ class RestoreCase:
     """A compressed prefix (one blob per layer) and a paged bf16 target cache."""
 
     def __init__(self, fmt: str, layers: int, heads: int, head_dim: int, pool: int, pages: int,
-                 seed: int):
+                 seed: int, contiguous: bool = False):
         from korith_vllm_ext import _paged
 
         self.fmt, self.layers, self.pages, self.pool = fmt, layers, pages, pool
@@ -177,7 +177,8 @@ class RestoreCase:
             del src
         self.cache = [torch.empty(2, pool, 16, heads, head_dim, dtype=torch.bfloat16, device=DEV)
                       for _ in range(layers)]
-        self.ids = seeded_table(pool, pages, seed + 7)
+        self.ids = (torch.arange(pages, dtype=torch.int32) if contiguous
+                    else seeded_table(pool, pages, seed + 7))
         self.launch = _paged.PreparedCodecLaunch(
             "restore", self.layout, [self.blobs[l].data_ptr() for l in range(layers)], 2,
             _paged.cache_view(self.cache), self.ids)
@@ -389,6 +390,22 @@ class ConnectorCase:
         return self.layers * (lay.data_bytes + lay.scale_bytes +
                               2 * self.tokens * self.heads * self.head_dim * 2)
 
+    def codec_launch(self, meta, direction: str):
+        """The device work alone: one launch over every layer of the pool
+        entry of meta's request, a dequant-scatter into the warm request's
+        pages ("restore") or the quant-gather of the cold request's pages into
+        the same blobs ("save", rewriting what the save wrote)."""
+        from korith_vllm_ext import _paged
+
+        pool = self.conn._pool
+        req = meta.requests[0]
+        entry = pool.get(req.prefix_hash)
+        bases = [pool._slab_ptr[b.layer_id] + b.data_offset for b in entry.blocks]
+        ids = (req.slot_mapping[::16][:entry.layout.n_pages] // 16).to(torch.int32)
+        caches = self.target if direction == "restore" else self.cache
+        return _paged.PreparedCodecLaunch(direction, entry.layout, bases, 2,
+                                          _paged.cache_view(caches), ids)
+
     def slot_launch(self, seed: int = 5):
         """Raw token-slot gather of `tokens` unordered slots of every plane."""
         from korith_vllm_ext import _paged
@@ -420,6 +437,14 @@ class ConnectorCase:
         save_ms = wall(lambda: self.save(smeta))
         lmeta = self.load_meta()
         load_ms = wall(lambda: self.load(lmeta))
+        side = self.conn._side_load
+        self.conn._side_load = False
+        load_current_ms = wall(lambda: self.load(lmeta))
+        self.conn._side_load = side
+        kernel_ms = time_launches(self.codec_launch(lmeta, "restore").launch, steps,
+                                  warmup).median_ms
+        save_kernel_ms = time_launches(self.codec_launch(smeta, "save").launch, steps,
+                                       warmup).median_ms
         algo = self.algo_bytes()
         fn, moved, keep = self.slot_launch()
         slot_ms = time_launches(fn, steps, warmup).median_ms
@@ -429,6 +454,12 @@ class ConnectorCase:
                 "scheduler_meta_ms": round(meta_ms, 4),
                 "save_ms": round(save_ms, 4), "save_GB/s": round(algo / save_ms / 1e6, 1),
                 "load_ms": round(load_ms, 4), "load_GB/s": round(algo / load_ms / 1e6, 1),
+                "save_kernel_ms": round(save_kernel_ms, 4),
+                "save_over_kernel": round(save_ms / save_kernel_ms, 3),
+                "load_current_stream_ms": round(load_current_ms, 4),
+                "restore_kernel_ms": round(kernel_ms, 4),
+                "load_over_kernel": round(load_ms / kernel_ms, 3),
+                "load_current_stream_over_kernel": round(load_current_ms / kernel_ms, 3),
                 "slot_gather_unordered_ms": round(slot_ms, 4),
                 "slot_gather_GB/s": round(moved / slot_ms / 1e6, 1),
                 "slot_gather_frac": round(moved / slot_ms / 1e6 / HBM_PEAK_GBS, 4)}
@@ -837,6 +868,27 @@ def run_profile(name: str, steps: int, warmup: int) -> int:
         log(f"copy: {t.mean_ms:.4f} ms/launch, 1 GiB read + 1 GiB written per launch, "
             f"{2 * 2**30 / t.mean_ms / 1e6:.1f} GB/s")
         return 0
+    if name in ("page_scatter_8b", "page_scatter_8b_contig"):
+        # the FP8 restore's destination pattern without the codec: 64 planes x
+        # 512 pages of 32 KiB from a dense source into an 8192-page bf16 cache
+        from korith_vllm_ext import _paged
+
+        src = torch.empty(64, 512, 16, 8, 128, dtype=torch.bfloat16, device=DEV).fill_(1.0)
+        cache = [torch.empty(2, 8192, 16, 8, 128, dtype=torch.bfloat16, device=DEV)
+                 for _ in range(32)]
+        ids = (torch.arange(512, dtype=torch.int32) if name.endswith("contig")
+               else seeded_table(8192, 512, 9))
+        view = _paged.cache_view(cache)
+        ins = [src[i].data_ptr() for i in range(64)]
+        fn = lambda: _paged.scatter_pages(ins, view.page_bytes, view, ids, 512)
+        t = time_launches(fn, steps, warmup)
+        log(f"{name}: {t.leg(2 * 64 * 512 * view.page_bytes)}")
+        return 0
+    if name == "fp8_restore_contig":
+        case = RestoreCase("fp8_e4m3_ph", 32, 8, 128, 8192, 512, 2, contiguous=True)
+        t = time_launches(case.launch.launch, steps, warmup)
+        log(f"{name}: {t.leg(case.algo_bytes)}")
+        return 0
     if name in ("raw_gather", "raw_scatter"):
         rc = RawCase()
         t = time_launches(rc.rotating(rc.gather if name == "raw_gather" else rc.scatter), steps,
@@ -877,7 +929,8 @@ def run_profile(name: str, steps: int, warmup: int) -> int:
 
 PROFILES = ["fp8_restore", "int4_restore", "fp8_save", "int4_save", "fp8_tensor_save",
             "fp8_restore_70b", "decode_70b", "decode_mfma", "decode_valu", "copy", "slot_copy",
-            "raw_gather", "raw_scatter"]
+            "raw_gather", "raw_scatter", "page_scatter_8b", "page_scatter_8b_contig",
+            "fp8_restore_contig"]
 
 
 def main() -> int:

@@ -54,13 +54,19 @@ def test_allocator_first_fit_and_coalesce():
 
 
 def test_allocator_prunes_completed_fences():
+    """Merged runs keep their fences (duplicates dropped); once a run holds
+    many, the completed ones are queried out, the pending ones kept."""
     a = _SlabAllocator(8)
     s, _ = a.alloc(4)
     t, _ = a.alloc(4)
-    a.free(s, 4, [FakeEvent(done=True)])
-    a.free(t, 4, [FakeEvent(done=False)])
+    done, pending = FakeEvent(done=True), FakeEvent(done=False)
+    a.free(s, 4, [done, done])
+    a.free(t, 4, [pending])
     start, fences = a.alloc(8)
-    assert start == 0 and len(fences) == 1 and fences[0].done is False
+    assert start == 0 and fences == [done, pending]
+    a.free(0, 8, [FakeEvent(done=True) for _ in range(9)] + [pending])
+    _, fences = a.alloc(8)
+    assert fences == [pending]
     a.free(0, 8)
     a.reset(5)
     assert a.runs() == [(5, 3)]
