@@ -145,6 +145,21 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
   return __builtin_bit_cast(uint16_t, (__bf16)x);
 }
 
+// Two fp32 values as one packed bf16 pair (RNE, one v_cvt_pk_bf16_f32).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
+// (a, b) as a bf16 hi pair plus the bf16 pair of what the hi parts leave
+// (a - hi_a, b - hi_b, exact in fp32): about 16 significant bits each.
+__device__ __forceinline__ void pk_bf16_hilo(float a, float b, uint32_t* hi, uint32_t* lo) {
+  const uint32_t h = pk_bf16(a, b);
+  *hi = h;
+  *lo = pk_bf16(a - u2f(h << 16), b - u2f(h & 0xFFFF0000u));
+}
+
 // a * b with +0 * x = +0 for every x (v_mul_legacy_f32); otherwise IEEE.
 __device__ __forceinline__ float mul_legacy(float a, float b) {
   float r;
@@ -331,9 +346,14 @@ __device__ __forceinline__ void mfma_chunk(
         cacc = mfma_bf16(qa_hi[T][st], kb[st], cacc);
         if constexpr (!QBF16) cacc = mfma_bf16(qa_lo[T][st], kb[st], cacc);
       }
-      float sc = 0.0f;
+      // One fma chain over the four groups (no zero seed: -0 + 0 would not fold).
+      float sc = kz[0] * qsum[T][0];
+      sc = __builtin_fmaf(ks[0], cacc[0], sc);
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) sc += ks[gi] * cacc[gi] + kz[gi] * qsum[T][gi];
+      for (int gi = 1; gi < 4; ++gi) {
+        sc = __builtin_fmaf(kz[gi], qsum[T][gi], sc);
+        sc = __builtin_fmaf(ks[gi], cacc[gi], sc);
+      }
       x[T][u] = valid ? sc * a.qk_scale_log2 : -__builtin_inff();
     }
   }
@@ -341,11 +361,14 @@ __device__ __forceinline__ void mfma_chunk(
   float p[NT][2];
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
-    const float cm = row_max16(fmaxf(x[T][0], x[T][1]));
     // Lazy rescale: the reference max moves only when a score exceeds it by
     // more than kRescaleSlack (p stays <= 2^kRescaleSlack), so the
-    // accumulators are rescaled a few times per split, not every chunk.
-    if (__any(cm > m_run[T] + kRescaleSlack)) {
+    // accumulators are rescaled a few times per split, not every chunk.  A
+    // lane compare and a wave vote decide that; the row maximum is only
+    // taken when some score does exceed it.
+    const float xm = fmaxf(x[T][0], x[T][1]);
+    if (__any(xm > m_run[T] + kRescaleSlack)) {
+      const float cm = row_max16(xm);
       const float m_new = fmaxf(m_run[T], cm);
       const float alpha = exp2_fast(m_run[T] - m_new);
       l_run[T] *= alpha;
@@ -383,7 +406,7 @@ __device__ __forceinline__ void mfma_chunk(
     // bytes, and the legacy multiply (+0 * x = +0 for every x, NaN and
     // infinities included) keeps them out of w and of the zero-point term.
     float wk[8];
-    float cs = 0.0f;
+    float cs = corr[T];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float sv = pscale(pw[e]);
@@ -393,11 +416,12 @@ __device__ __forceinline__ void mfma_chunk(
     u32x4 ahi, alo;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t hw = pack2<true>(wk[2 * j], wk[2 * j + 1]);
-      ahi[j] = hw;
-      alo[j] = pack2<true>(wk[2 * j] - u2f(hw << 16), wk[2 * j + 1] - u2f(hw & 0xFFFF0000u));
+      uint32_t h, l;
+      pk_bf16_hilo(wk[2 * j], wk[2 * j + 1], &h, &l);
+      ahi[j] = h;
+      alo[j] = l;
     }
-    corr[T] += cs;
+    corr[T] = cs;
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       acc[T][b] = mfma_bf16(ahi, vb[b], acc[T][b]);
@@ -463,10 +487,10 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
       u32x4 vh, vl;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float x0 = xq[nib_of_k(2 * j)], x1 = xq[nib_of_k(2 * j + 1)];
-        const uint32_t hw = pack2<true>(x0, x1);
-        vh[j] = mine ? hw : 0u;
-        vl[j] = mine ? pack2<true>(x0 - u2f(hw << 16), x1 - u2f(hw & 0xFFFF0000u)) : 0u;
+        uint32_t h, l;
+        pk_bf16_hilo(xq[nib_of_k(2 * j)], xq[nib_of_k(2 * j + 1)], &h, &l);
+        vh[j] = mine ? h : 0u;
+        vl[j] = mine ? l : 0u;
       }
       qa_hi[T][st] = vh;
       qa_lo[T][st] = vl;
