@@ -11,7 +11,8 @@
 // Work item: one wave per (sequence, KV head, split of split_tokens tokens);
 // grid = (num_kv_heads, max_splits, num_seqs), or (max_splits, num_kv_heads,
 // num_seqs) past 65535 splits.  The wave walks its split in chunks of 32
-// tokens (two 16-token pages) and keeps, per query head of the GQA group, a
+// tokens (two 16-token pages), streamed through a small per-wave LDS ring by
+// non-temporal LDS DMA, and keeps, per query head of the GQA group, a
 // running max m (log2 domain), sum l and an unnormalised output.
 // A second kernel merges the splits.
 //
@@ -221,32 +222,78 @@ __device__ __forceinline__ int64_t page_of(const DecodeArgs& a, const int32_t* b
   return *ok ? (int64_t)v : 0;
 }
 
-// Loads of one 32-token chunk (two pages) for the MFMA lane layout.
+// One 32-token chunk (two pages) in the MFMA lane layout.
 struct ChunkLoads {
   u32x4 kcode[2], kpar[2];  // K codes / params of page u: lane (t = lo, j = hi)
   u32x4 vc0, vc1;           // V codes: lane (dim block lo, tokens 8 hi .. 8 hi + 7)
   u32x4 vp0, vp1;           // V params of group lo % 4 for those 8 tokens
 };
 
-__device__ __forceinline__ ChunkLoads issue_chunk(const DecodeArgs& a, int64_t pg0, int64_t pg1,
-                                                  int h, int lo, int hi) {
+// The chunks of a split stream through a per-wave LDS ring.  A slot holds
+// the K codes of page 0 and 1 (1 KiB each, [0, 2048)), their V codes
+// ([2048, 4096)) and the four 256-byte parameter blocks K0, K1, V0, V1
+// ([4096, 5120)).  Each block arrives by one LDS DMA (global_load_lds_dwordx4,
+// non-temporal: every line is read once, by one instruction); DMA lane L
+// writes slot bytes [16 L, 16 L + 16), and its source address is chosen so
+// that the compute lanes' reads in read_chunk are consecutive 16-byte slots
+// (no bank conflicts).  No load registers are held while a chunk is in
+// flight, so a wave keeps several chunks in flight at any occupancy.
+constexpr int kSlotBytes = 5120;
+constexpr int kDmaNonTemporal = 2;  // aux bits of the LDS DMA: nt
+
+__device__ __forceinline__ void lds_dma16(const void* g, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(g),
+                                   (__attribute__((address_space(3))) uint32_t*)lds, 16, 0,
+                                   kDmaNonTemporal);
+}
+
+__device__ __forceinline__ void dma_chunk(const DecodeArgs& a, int64_t pg0, int64_t pg1, int h,
+                                          int lane, uint8_t* slot) {
+  const int lo = lane & 15, hi = lane >> 4;
+  const int64_t H = a.num_kv_heads, hb0 = pg0 * H + h, hb1 = pg1 * H + h;
+  // K: compute lane (t = lo, j = hi) reads slot lane; it needs code bytes
+  // 64 t + 16 j .. + 15 of the (page, head) block.
+  const int koff = lo * 64 + hi * 16;
+  // V: compute lane (lo, hi) needs the 32 bytes 64 lo + 32 (hi & 1) of page
+  // hi >> 1, as halves j = 0, 1 in slots lo + 16 (hi & 1) + 32 j of that page.
+  const int voff = 64 * lo + 32 * (hi & 1) + 16 * (hi >> 1);
+  lds_dma16(a.kc + hb0 * kHBCodes + koff, slot);
+  lds_dma16(a.kc + hb1 * kHBCodes + koff, slot + 1024);
+  lds_dma16(a.vc + hb0 * kHBCodes + voff, slot + 2048);
+  lds_dma16(a.vc + hb1 * kHBCodes + voff, slot + 3072);
+  // params: lanes 16 q .. 16 q + 15 copy block q = (K0, K1, V0, V1) as is.
+  const uint32_t* pb = (hi >> 1) ? a.vp : a.kp;
+  lds_dma16(pb + ((hi & 1) ? hb1 : hb0) * kHBParams + lo * 4, slot + 4096);
+}
+
+__device__ __forceinline__ ChunkLoads read_chunk(const uint8_t* slot, int lane) {
+  const int lo = lane & 15, hi = lane >> 4;
   ChunkLoads c;
-  const int H = a.num_kv_heads;
-  const int64_t hb0 = pg0 * H + h, hb1 = pg1 * H + h;
-  c.kcode[0] = *reinterpret_cast<const u32x4*>(a.kc + hb0 * kHBCodes + lo * 64 + hi * 16);
-  c.kcode[1] = *reinterpret_cast<const u32x4*>(a.kc + hb1 * kHBCodes + lo * 64 + hi * 16);
-  c.kpar[0] = *reinterpret_cast<const u32x4*>(a.kp + hb0 * kHBParams + lo * 4);
-  c.kpar[1] = *reinterpret_cast<const u32x4*>(a.kp + hb1 * kHBParams + lo * 4);
-  const int64_t vhb = (hi >> 1) ? hb1 : hb0;
-  const u32x4* vcp =
-      reinterpret_cast<const u32x4*>(a.vc + vhb * kHBCodes + 64 * lo + 32 * (hi & 1));
-  c.vc0 = vcp[0];
-  c.vc1 = vcp[1];
-  const u32x4* vpp =
-      reinterpret_cast<const u32x4*>(a.vp + vhb * kHBParams + (lo & 3) * 16 + 8 * (hi & 1));
-  c.vp0 = vpp[0];
-  c.vp1 = vpp[1];
+  c.kcode[0] = *reinterpret_cast<const u32x4*>(slot + lane * 16);
+  c.kcode[1] = *reinterpret_cast<const u32x4*>(slot + 1024 + lane * 16);
+  c.kpar[0] = *reinterpret_cast<const u32x4*>(slot + 4096 + lo * 16);
+  c.kpar[1] = *reinterpret_cast<const u32x4*>(slot + 4096 + 256 + lo * 16);
+  const uint8_t* vs = slot + 2048 + 1024 * (hi >> 1) + (lo + 16 * (hi & 1)) * 16;
+  c.vc0 = *reinterpret_cast<const u32x4*>(vs);
+  c.vc1 = *reinterpret_cast<const u32x4*>(vs + 512);
+  const uint8_t* ps = slot + 4096 + 512 + 256 * (hi >> 1) + ((lo & 3) * 16 + 8 * (hi & 1)) * 4;
+  c.vp0 = *reinterpret_cast<const u32x4*>(ps);
+  c.vp1 = *reinterpret_cast<const u32x4*>(ps + 16);
   return c;
+}
+
+// Waits until at most `newer` chunks' DMAs (issued after the one about to be
+// read) are outstanding; vmcnt counts this wave's vector-memory instructions
+// in issue order and the loop issues nothing else.  The compiler does not
+// order LDS reads after LDS DMAs by itself, so the memory clobber also keeps
+// read_chunk below the wait.
+template <int D>
+__device__ __forceinline__ void dma_wait(int newer) {
+  static_assert(D >= 2 && D <= 4, "ring depth");
+  if (D >= 4 && newer >= 3) asm volatile("s_waitcnt vmcnt(15)" ::: "memory");
+  else if (D >= 3 && newer >= 2) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+  else if (newer >= 1) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Block-table entries of a split (at most 64 pages: split_tokens <= 1024),
@@ -259,7 +306,7 @@ struct SplitPages {
 // Lane's raw block-table entry of split sp, read before the context length
 // is known (so the two loads overlap); bounded by the table's row only.
 __device__ __forceinline__ int split_table_entry(const DecodeArgs& a, const int32_t* bt, int sp) {
-  const int first = sp * (a.split_tokens / kBS), lane = threadIdx.x;
+  const int first = sp * (a.split_tokens / kBS), lane = threadIdx.x & 63;
   return (lane < a.split_tokens / kBS && first + lane < a.bt_stride) ? bt[first + lane] : -1;
 }
 
@@ -272,7 +319,7 @@ __device__ __forceinline__ SplitPages split_pages(const DecodeArgs& a, int raw, 
   sp.first = tok_begin / kBS;
   const int n = (tok_end - tok_begin + kBS - 1) / kBS;
   int v = -1;
-  if ((int)threadIdx.x < n) {
+  if ((int)(threadIdx.x & 63) < n) {
     v = raw;
     if (v < 0 || (int64_t)v >= a.pool_pages) {
       if (a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_BLOCK_RANGE);
@@ -437,7 +484,14 @@ __device__ __forceinline__ void mfma_chunk(
 #define AMF_DECODE_WAVES_PER_EU 2
 #endif
 
-template <int R, bool QBF16>
+// D: chunks in the LDS ring (D - 1 in flight while one computes).
+#ifndef AMF_DECODE_RING_SMALL_GQA
+#define AMF_DECODE_RING_SMALL_GQA 2
+#endif
+#ifndef AMF_DECODE_RING_GQA8
+#define AMF_DECODE_RING_GQA8 3
+#endif
+template <int R, bool QBF16, int D = (R > 4 ? AMF_DECODE_RING_GQA8 : AMF_DECODE_RING_SMALL_GQA)>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(AMF_DECODE_WAVES_PER_EU)))
 void int4_decode_mfma_kernel(DecodeArgs a) {
   constexpr int NT = (R + 3) / 4;  // 16-row tiles of (head, group) pairs
@@ -522,25 +576,30 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
   }
   __shared__ __attribute__((aligned(16))) float p_lds[NT][2][4][16];
 
-  // Software pipeline: the next chunk's pages are in flight while the current
-  // chunk computes.  The last iteration re-loads its own chunk (clamped).
+  // Ring pipeline: chunks c + 1 .. c + D - 1 are in flight while chunk c
+  // computes.
+  __shared__ __attribute__((aligned(16))) uint8_t ring[D][kSlotBytes];
   const SplitPages spg = split_pages(a, bt_raw, tok_begin, tok_end);
-  const int last_c0 = tok_begin + ((tok_end - tok_begin - 1) / 32) * 32;
-  bool pok_n[2];
-  int64_t pg_n[2];
-  pg_n[0] = split_page(spg, tok_begin / kBS, &pok_n[0]);
-  pg_n[1] = split_page(spg, tok_begin / kBS + 1, &pok_n[1]);
-  ChunkLoads nxt = issue_chunk(a, pg_n[0], pg_n[1], h, lo, hi);
-
-  for (int c0 = tok_begin; c0 < tok_end; c0 += 32) {
-    const ChunkLoads cur = nxt;
-    const bool pok[2] = {pok_n[0], pok_n[1]};
-    const int cn = c0 + 32 <= last_c0 ? c0 + 32 : c0;
-    pg_n[0] = split_page(spg, cn / kBS, &pok_n[0]);
-    pg_n[1] = split_page(spg, cn / kBS + 1, &pok_n[1]);
-    nxt = issue_chunk(a, pg_n[0], pg_n[1], h, lo, hi);
-    mfma_chunk<R, QBF16>(a, cur, pok, c0, tok_end, lo, hi, qa_hi, qa_lo, qsum, m_run, l_run,
-                         corr, acc, p_lds);
+  const int nch = (tok_end - tok_begin + 31) / 32;
+  const int pi0 = tok_begin / kBS;
+  auto issue = [&](int c) {
+    bool ok;
+    const int64_t p0 = split_page(spg, pi0 + 2 * c, &ok);
+    const int64_t p1 = split_page(spg, pi0 + 2 * c + 1, &ok);
+    dma_chunk(a, p0, p1, h, lane, ring[c % D]);
+  };
+#pragma unroll
+  for (int k = 0; k + 1 < D; ++k)
+    if (k < nch) issue(k);
+  for (int c = 0; c < nch; ++c) {
+    if (c + D - 1 < nch) issue(c + D - 1);
+    dma_wait<D>(min(D - 1, nch - 1 - c));
+    const ChunkLoads cur = read_chunk(ring[c % D], lane);
+    bool pok[2];
+    split_page(spg, pi0 + 2 * c, &pok[0]);
+    split_page(spg, pi0 + 2 * c + 1, &pok[1]);
+    mfma_chunk<R, QBF16>(a, cur, pok, tok_begin + 32 * c, tok_end, lo, hi, qa_hi, qa_lo, qsum,
+                         m_run, l_run, corr, acc, p_lds);
   }
 
   // ---- write the split's partial (unnormalised O, m, l) ----
