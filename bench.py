@@ -968,9 +968,11 @@ def main() -> int:
     log("c2 fp8 restore: building inputs")
     fp8 = RestoreCase("fp8_e4m3_ph", 32, 8, 128, 8192, 512, seed=2)
     t = time_launches(fp8.launch.launch, args.steps, args.warmup)
-    ms = t.mean_ms
+    # GB/s on the median per-launch time (the mean of the whole timed region,
+    # which also carries the per-launch event records, is reported beside it).
+    ms = t.median_ms
     gbs = fp8.algo_bytes / (ms * 1e-3) / 1e9
-    log(f"c2 fp8 restore: mean {ms:.4f} ms, median {t.median_ms:.4f} ms, {gbs:.1f} GB/s")
+    log(f"c2 fp8 restore: mean {t.mean_ms:.4f} ms, median {ms:.4f} ms, {gbs:.1f} GB/s")
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -979,6 +981,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "ms_per_step_mean": round(t.mean_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
