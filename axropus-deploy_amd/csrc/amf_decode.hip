@@ -222,20 +222,13 @@ __device__ __forceinline__ int64_t page_of(const DecodeArgs& a, const int32_t* b
   return *ok ? (int64_t)v : 0;
 }
 
-// One 32-token chunk (two pages) in the MFMA lane layout.
-struct ChunkLoads {
-  u32x4 kcode[2], kpar[2];  // K codes / params of page u: lane (t = lo, j = hi)
-  u32x4 vc0, vc1;           // V codes: lane (dim block lo, tokens 8 hi .. 8 hi + 7)
-  u32x4 vp0, vp1;           // V params of group lo % 4 for those 8 tokens
-};
-
 // The chunks of a split stream through a per-wave LDS ring.  A slot holds
 // the K codes of page 0 and 1 (1 KiB each, [0, 2048)), their V codes
 // ([2048, 4096)) and the four 256-byte parameter blocks K0, K1, V0, V1
 // ([4096, 5120)).  Each block arrives by one LDS DMA (global_load_lds_dwordx4,
 // non-temporal: every line is read once, by one instruction); DMA lane L
 // writes slot bytes [16 L, 16 L + 16), and its source address is chosen so
-// that the compute lanes' reads in read_chunk are consecutive 16-byte slots
+// that the compute lanes' reads (read_chunk_k, read_chunk_v) are consecutive 16-byte slots
 // (no bank conflicts).  No load registers are held while a chunk is in
 // flight, so a wave keeps several chunks in flight at any occupancy.
 constexpr int kSlotBytes = 5120;
@@ -266,27 +259,35 @@ __device__ __forceinline__ void dma_chunk(const DecodeArgs& a, int64_t pg0, int6
   lds_dma16(pb + ((hi & 1) ? hb1 : hb0) * kHBParams + lo * 4, slot + 4096);
 }
 
-__device__ __forceinline__ ChunkLoads read_chunk(const uint8_t* slot, int lane) {
+// Operands of one chunk from its slot, in the MFMA lane layout.  K: codes
+// and params of page u for lane (t = lo, j = hi).  V: codes of dim block lo
+// for tokens 8 hi .. 8 hi + 7 (halves 0 and 1: dims 0-3 and 4-7 of the
+// block), and the params of group lo % 4 for those tokens.
+__device__ __forceinline__ void read_chunk_k(const uint8_t* slot, int lane, u32x4 (&kcode)[2],
+                                             u32x4 (&kpar)[2]) {
+  const int lo = lane & 15;
+  kcode[0] = *reinterpret_cast<const u32x4*>(slot + lane * 16);
+  kcode[1] = *reinterpret_cast<const u32x4*>(slot + 1024 + lane * 16);
+  kpar[0] = *reinterpret_cast<const u32x4*>(slot + 4096 + lo * 16);
+  kpar[1] = *reinterpret_cast<const u32x4*>(slot + 4096 + 256 + lo * 16);
+}
+
+__device__ __forceinline__ void read_chunk_v(const uint8_t* slot, int lane, u32x4* vc0,
+                                             u32x4* vc1, u32x4* vp0, u32x4* vp1) {
   const int lo = lane & 15, hi = lane >> 4;
-  ChunkLoads c;
-  c.kcode[0] = *reinterpret_cast<const u32x4*>(slot + lane * 16);
-  c.kcode[1] = *reinterpret_cast<const u32x4*>(slot + 1024 + lane * 16);
-  c.kpar[0] = *reinterpret_cast<const u32x4*>(slot + 4096 + lo * 16);
-  c.kpar[1] = *reinterpret_cast<const u32x4*>(slot + 4096 + 256 + lo * 16);
   const uint8_t* vs = slot + 2048 + 1024 * (hi >> 1) + (lo + 16 * (hi & 1)) * 16;
-  c.vc0 = *reinterpret_cast<const u32x4*>(vs);
-  c.vc1 = *reinterpret_cast<const u32x4*>(vs + 512);
+  *vc0 = *reinterpret_cast<const u32x4*>(vs);
+  *vc1 = *reinterpret_cast<const u32x4*>(vs + 512);
   const uint8_t* ps = slot + 4096 + 512 + 256 * (hi >> 1) + ((lo & 3) * 16 + 8 * (hi & 1)) * 4;
-  c.vp0 = *reinterpret_cast<const u32x4*>(ps);
-  c.vp1 = *reinterpret_cast<const u32x4*>(ps + 16);
-  return c;
+  *vp0 = *reinterpret_cast<const u32x4*>(ps);
+  *vp1 = *reinterpret_cast<const u32x4*>(ps + 16);
 }
 
 // Waits until at most `newer` chunks' DMAs (issued after the one about to be
 // read) are outstanding; vmcnt counts this wave's vector-memory instructions
 // in issue order and the loop issues nothing else.  The compiler does not
 // order LDS reads after LDS DMAs by itself, so the memory clobber also keeps
-// read_chunk below the wait.
+// the chunk's LDS reads below the wait.
 template <int D>
 __device__ __forceinline__ void dma_wait(int newer) {
   static_assert(D >= 2 && D <= 4, "ring depth");
@@ -360,16 +361,18 @@ constexpr float kRescaleSlack = AMF_DECODE_RESCALE_SLACK;  // log2 units
 
 template <int R, bool QBF16>
 __device__ __forceinline__ void mfma_chunk(
-    const DecodeArgs& a, const ChunkLoads& cur, const bool (&pok)[2], int c0, int tok_end, int lo,
+    const DecodeArgs& a, const uint8_t* slot, const bool (&pok)[2], int c0, int tok_end, int lo,
     int hi, const u32x4 (&qa_hi)[(R + 3) / 4][4], const u32x4 (&qa_lo)[(R + 3) / 4][4],
     const float (&qsum)[(R + 3) / 4][4], float (&m_run)[(R + 3) / 4], float (&l_run)[(R + 3) / 4],
     float (&corr)[(R + 3) / 4], f32x4 (&acc)[(R + 3) / 4][8],
     float (&p_lds)[(R + 3) / 4][2][4][16]) {
   constexpr int NT = (R + 3) / 4;
-  const u32x4* kcode = cur.kcode;
-  const u32x4* kpar = cur.kpar;
+  const int lane = lo + 16 * hi;
   const int vu = hi >> 1, vhalf = hi & 1;
-  const u32x4 vc0 = cur.vc0, vc1 = cur.vc1, vp0 = cur.vp0, vp1 = cur.vp1;
+  // K operands now; the V side is read from the slot just before the PV
+  // product, so its registers are not live across QK^T and the softmax.
+  u32x4 kcode[2], kpar[2];
+  read_chunk_k(slot, lane, kcode, kpar);
 
   // ---- QK^T and online softmax ----
   float x[NT][2];
@@ -434,13 +437,10 @@ __device__ __forceinline__ void mfma_chunk(
   __builtin_amdgcn_wave_barrier();
 
   // ---- PV ----
-  u32x4 vb[8];
-  {
-    const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
-#pragma unroll
-    for (int b = 0; b < 8; ++b) vb[b] = nib8_to_bf16_128c(vw[b]);
-  }
+  u32x4 vc0, vc1, vp0, vp1;
+  read_chunk_v(slot, lane, &vc0, &vc1, &vp0, &vp1);
   const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
+  u32x4 ahi[NT], alo[NT];
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
     // A row (r', g) = (4T + lo/4, lo%4), k-slice hi: tokens 8 hi .. 8 hi + 7.
@@ -460,20 +460,24 @@ __device__ __forceinline__ void mfma_chunk(
       wk[k_of_nib(e)] = mul_legacy(pv[e], sv);
       cs += mul_legacy(pv[e], pzero(pw[e]) - kCodeBias * sv);
     }
-    u32x4 ahi, alo;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t h, l;
       pk_bf16_hilo(wk[2 * j], wk[2 * j + 1], &h, &l);
-      ahi[j] = h;
-      alo[j] = l;
+      ahi[T][j] = h;
+      alo[T][j] = l;
     }
     corr[T] = cs;
+  }
+  // Dim block outermost: one block's code operand is live at a time.
+  const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      acc[T][b] = mfma_bf16(ahi, vb[b], acc[T][b]);
-      acc[T][b] = mfma_bf16(alo, vb[b], acc[T][b]);
-    }
+  for (int b = 0; b < 8; ++b) {
+    const u32x4 vb = nib8_to_bf16_128c(vw[b]);
+#pragma unroll
+    for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(ahi[T], vb, acc[T][b]);
+#pragma unroll
+    for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(alo[T], vb, acc[T][b]);
   }
   __builtin_amdgcn_wave_barrier();
 }
@@ -594,12 +598,11 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
   for (int c = 0; c < nch; ++c) {
     if (c + D - 1 < nch) issue(c + D - 1);
     dma_wait<D>(min(D - 1, nch - 1 - c));
-    const ChunkLoads cur = read_chunk(ring[c % D], lane);
     bool pok[2];
     split_page(spg, pi0 + 2 * c, &pok[0]);
     split_page(spg, pi0 + 2 * c + 1, &pok[1]);
-    mfma_chunk<R, QBF16>(a, cur, pok, tok_begin + 32 * c, tok_end, lo, hi, qa_hi, qa_lo, qsum,
-                         m_run, l_run, corr, acc, p_lds);
+    mfma_chunk<R, QBF16>(a, ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa_hi, qa_lo,
+                         qsum, m_run, l_run, corr, acc, p_lds);
   }
 
   // ---- write the split's partial (unnormalised O, m, l) ----
