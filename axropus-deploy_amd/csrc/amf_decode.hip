@@ -119,6 +119,11 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // element order is k = [n0 n2 n4 n6 n1 n3 n5 n7] (kNibOfK below); the other
 // operand of the product is laid out in the same order.
 constexpr float kCodeBias = 128.0f;
+// The PV accumulators hold O * kPvScale (fp16 subnormal codes are c * 2^-24).
+constexpr float kPvScale = 0x1p-24f;
+// fp16 bit patterns bounding the V scales of the fp16 PV path: [2^-10, 255].
+constexpr uint32_t kF16ScaleMinBits = 0x1400u;  // 2^-10
+constexpr uint32_t kF16ScaleMaxBits = 0x5BF8u;  // 255
 
 __device__ __forceinline__ u32x4 nib8_to_bf16_128c(uint32_t w) {
   const uint32_t ev = w & 0x0F0F0F0Fu;          // bytes: n0 n2 n4 n6
@@ -151,6 +156,27 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
+// Two fp32 values as one packed fp16 pair (RNE, one v_cvt_pk_f16_f32).
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint32_t pk_f16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+}
+
+__device__ __forceinline__ f32x4 mfma_f16(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// 8 nibbles of w (tokens 0..7 of one V dim) -> fp16 PV operand in the k
+// order [t0 t4 t1 t5 t2 t6 t3 t7], as subnormals: even tokens c * 2^-24, odd
+// tokens 16 c * 2^-24 (the nibble left where it sits; the matching weights
+// carry 1/16).  Exact inputs, no bias term; five ops per 8 codes.
+__device__ __forceinline__ u32x4 nib8_to_f16_sub(uint32_t w) {
+  const uint32_t w8 = w >> 8;
+  return u32x4{w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u};
 }
 
 // (a, b) as a bf16 hi pair plus the bf16 pair of what the hi parts leave
@@ -353,14 +379,15 @@ __device__ __forceinline__ int work_split(const DecodeArgs& a) {
 
 // ============================================================== MFMA path ==
 
-// One 32-token chunk of the MFMA kernel: QK^T, online softmax, PV.
+// One 32-token chunk of the MFMA kernel, in two steps: chunk_qk (QK^T and the
+// online softmax, leaving the weights p in p_lds) and chunk_pv (PV).
 #ifndef AMF_DECODE_RESCALE_SLACK
 #define AMF_DECODE_RESCALE_SLACK 8.0f
 #endif
 constexpr float kRescaleSlack = AMF_DECODE_RESCALE_SLACK;  // log2 units
 
 template <int R, bool QBF16>
-__device__ __forceinline__ void mfma_chunk(
+__device__ __forceinline__ void chunk_qk(
     const DecodeArgs& a, const uint8_t* slot, const bool (&pok)[2], int c0, int tok_end, int lo,
     int hi, const u32x4 (&qa_hi)[(R + 3) / 4][4], const u32x4 (&qa_lo)[(R + 3) / 4][4],
     const float (&qsum)[(R + 3) / 4][4], float (&m_run)[(R + 3) / 4], float (&l_run)[(R + 3) / 4],
@@ -368,8 +395,7 @@ __device__ __forceinline__ void mfma_chunk(
     float (&p_lds)[(R + 3) / 4][2][4][16]) {
   constexpr int NT = (R + 3) / 4;
   const int lane = lo + 16 * hi;
-  const int vu = hi >> 1, vhalf = hi & 1;
-  // K operands now; the V side is read from the slot just before the PV
+  // K operands only; the V side is read from the slot just before the PV
   // product, so its registers are not live across QK^T and the softmax.
   u32x4 kcode[2], kpar[2];
   read_chunk_k(slot, lane, kcode, kpar);
@@ -435,49 +461,97 @@ __device__ __forceinline__ void mfma_chunk(
     p_lds[T][1][hi][lo] = p[T][1];
   }
   __builtin_amdgcn_wave_barrier();
+}
 
-  // ---- PV ----
-  u32x4 vc0, vc1, vp0, vp1;
-  read_chunk_v(slot, lane, &vc0, &vc1, &vp0, &vp1);
+// Whether a chunk's V scales allow the fp16 PV path (see chunk_pv): each lane
+// checks the scale words of its 8 tokens, then the wave votes.
+__device__ __forceinline__ bool pv_f16_ok(const u32x4& vp0, const u32x4& vp1) {
+  uint32_t smax = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) smax = max(smax, max(vp0[e] & 0xFFFFu, vp1[e] & 0xFFFFu));
+  return !__any(smax > kF16ScaleMaxBits || (smax != 0u && smax < kF16ScaleMinBits));
+}
+
+// PV of one chunk from its V operands (read_chunk_v) and the weights in p_lds.
+template <int R, bool F16>
+__device__ __forceinline__ void chunk_pv(const u32x4& vc0, const u32x4& vc1, const u32x4& vp0,
+                                         const u32x4& vp1, int lo, int hi,
+                                         float (&corr)[(R + 3) / 4], f32x4 (&acc)[(R + 3) / 4][8],
+                                         float (&p_lds)[(R + 3) / 4][2][4][16]) {
+  constexpr int NT = (R + 3) / 4;
+  const int vu = hi >> 1, vhalf = hi & 1;
   const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
-  u32x4 ahi[NT], alo[NT];
-#pragma unroll
-  for (int T = 0; T < NT; ++T) {
-    // A row (r', g) = (4T + lo/4, lo%4), k-slice hi: tokens 8 hi .. 8 hi + 7.
-    const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
-    const float4 pa = pl[0], pb = pl[1];
-    const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-    // Weights w = p * s of the lane's 8 tokens in the operand's k order, as a
-    // bf16 hi + lo pair.  A token outside the context or on a page with a bad
-    // id has p = +0 exactly (its score is -inf); its param words may hold any
-    // bytes, and the legacy multiply (+0 * x = +0 for every x, NaN and
-    // infinities included) keeps them out of w and of the zero-point term.
-    float wk[8];
-    float cs = corr[T];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float sv = pscale(pw[e]);
-      wk[k_of_nib(e)] = mul_legacy(pv[e], sv);
-      cs += mul_legacy(pv[e], pzero(pw[e]) - kCodeBias * sv);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t h, l;
-      pk_bf16_hilo(wk[2 * j], wk[2 * j + 1], &h, &l);
-      ahi[T][j] = h;
-      alo[T][j] = l;
-    }
-    corr[T] = cs;
-  }
-  // Dim block outermost: one block's code operand is live at a time.
   const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
+  // Both paths accumulate O * 2^-24 (restored by the partial write).
+  //  fp16: weights w = p * s as one fp16 each (about 11 bits), codes as exact
+  //   fp16 subnormals; one MFMA per tile.  Used for a chunk whose V scales all
+  //   lie in [2^-10, 255] or are 0 (pv_f16_ok), so no weight overflows
+  //   (p <= 2^8) and the chunk's largest weights stay normal fp16 numbers.
+  //  bf16: weights w * 2^-24 as a bf16 hi + lo pair (about 16 bits), codes as
+  //   the bf16 128 + c, so the zero-point term carries -128 s.
+  if constexpr (F16) {
+    u32x4 a16[NT];
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    const u32x4 vb = nib8_to_bf16_128c(vw[b]);
+    for (int T = 0; T < NT; ++T) {
+      // A row (r', g) = (4T + lo/4, lo%4), k-slice hi: tokens 8 hi .. 8 hi + 7.
+      const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
+      const float4 pa = pl[0], pb = pl[1];
+      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+      // A token outside the context or on a page with a bad id has p = +0
+      // exactly (its score is -inf); its param words may hold any bytes, and
+      // the legacy multiply (+0 * x = +0 for every x, NaN and infinities
+      // included) keeps them out of w and of the zero-point term.
+      float w[8];
+      float cs = corr[T];
 #pragma unroll
-    for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(ahi[T], vb, acc[T][b]);
+      for (int e = 0; e < 8; ++e) {
+        const float sv = pscale(pw[e]);
+        w[e] = mul_legacy(pv[e], (e & 1) ? sv * 0.0625f : sv);
+        cs += mul_legacy(pv[e], pzero(pw[e]));
+      }
+      a16[T] = u32x4{pk_f16(w[0], w[4]), pk_f16(w[1], w[5]), pk_f16(w[2], w[6]),
+                     pk_f16(w[3], w[7])};
+      corr[T] = cs;
+    }
+    // Dim block outermost: one block's code operand is live at a time.
 #pragma unroll
-    for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(alo[T], vb, acc[T][b]);
+    for (int b = 0; b < 8; ++b) {
+      const u32x4 vb = nib8_to_f16_sub(vw[b]);
+#pragma unroll
+      for (int T = 0; T < NT; ++T) acc[T][b] = mfma_f16(a16[T], vb, acc[T][b]);
+    }
+  } else {
+    u32x4 ahi[NT], alo[NT];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
+      const float4 pa = pl[0], pb = pl[1];
+      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+      float wk[8];
+      float cs = corr[T];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float sv = pscale(pw[e]);
+        wk[k_of_nib(e)] = mul_legacy(pv[e], sv * kPvScale);
+        cs += mul_legacy(pv[e], pzero(pw[e]) - kCodeBias * sv);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t h, l;
+        pk_bf16_hilo(wk[2 * j], wk[2 * j + 1], &h, &l);
+        ahi[T][j] = h;
+        alo[T][j] = l;
+      }
+      corr[T] = cs;
+    }
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const u32x4 vb = nib8_to_bf16_128c(vw[b]);
+#pragma unroll
+      for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(ahi[T], vb, acc[T][b]);
+#pragma unroll
+      for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(alo[T], vb, acc[T][b]);
+    }
   }
   __builtin_amdgcn_wave_barrier();
 }
@@ -595,14 +669,39 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
   for (int k = 0; k + 1 < D; ++k)
     if (k < nch) issue(k);
-  for (int c = 0; c < nch; ++c) {
-    if (c + D - 1 < nch) issue(c + D - 1);
+  // Chunks take the fp16 PV path until one whose V scales it cannot take;
+  // from that chunk on the split finishes on the bf16 path (a second loop, so
+  // that each loop keeps its own register footprint).
+  auto qk = [&](int c) {
     dma_wait<D>(min(D - 1, nch - 1 - c));
     bool pok[2];
     split_page(spg, pi0 + 2 * c, &pok[0]);
     split_page(spg, pi0 + 2 * c + 1, &pok[1]);
-    mfma_chunk<R, QBF16>(a, ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa_hi, qa_lo,
-                         qsum, m_run, l_run, corr, acc, p_lds);
+    chunk_qk<R, QBF16>(a, ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa_hi, qa_lo,
+                       qsum, m_run, l_run, corr, acc, p_lds);
+  };
+  int c = 0;
+  bool pending = false;  // chunk c has had QK^T and the softmax, not PV
+  for (; c < nch; ++c) {
+    if (c + D - 1 < nch) issue(c + D - 1);
+    qk(c);
+    u32x4 vc0, vc1, vp0, vp1;
+    read_chunk_v(ring[c % D], lane, &vc0, &vc1, &vp0, &vp1);
+    if (!pv_f16_ok(vp0, vp1)) {
+      pending = true;
+      break;
+    }
+    chunk_pv<R, true>(vc0, vc1, vp0, vp1, lo, hi, corr, acc, p_lds);
+  }
+  for (; c < nch; ++c) {
+    if (!pending) {
+      if (c + D - 1 < nch) issue(c + D - 1);
+      qk(c);
+    }
+    pending = false;
+    u32x4 vc0, vc1, vp0, vp1;
+    read_chunk_v(ring[c % D], lane, &vc0, &vc1, &vp0, &vp1);
+    chunk_pv<R, false>(vc0, vc1, vp0, vp1, lo, hi, corr, acc, p_lds);
   }
 
   // ---- write the split's partial (unnormalised O, m, l) ----
@@ -621,7 +720,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
       for (int b = 0; b < 8; ++b) {
         const f32x4 t = acc[T][b];
         const float v = gsel == 0 ? t[0] : gsel == 1 ? t[1] : gsel == 2 ? t[2] : t[3];
-        o[b] = v + cv;
+        o[b] = __builtin_fmaf(v, 1.0f / kPvScale, cv);
       }
       float* base = a.ws + (((int64_t)s * a.num_q_heads + (int64_t)h * R + r) * a.max_splits + sp) *
                                kPartStride;

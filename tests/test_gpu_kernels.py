@@ -538,6 +538,49 @@ def test_int4_paged_decode_peaked_scores(algo):
     check_attention(got, ref)
 
 
+@pytest.mark.parametrize("case", ["large", "small", "mixed"])
+def test_int4_paged_decode_scale_range_paths(case):
+    """The MFMA kernel's PV product takes fp16 weights for a 32-token chunk
+    whose V scales all lie in [2^-10, 255] and bf16 hi + lo weights otherwise.
+    V scaled x300 (scales above 255), x1e-5 (below 2^-10), and x300 on every
+    other page of each sequence (both paths inside one split) must all decode
+    to the float64 result, compared after dividing out the factor."""
+    R, Hkv, D, bs = 4, 2, 128, 16
+    ctxs = [37, 700, 1500, 300]
+    g = torch.Generator().manual_seed(141)
+    q = torch.randn(len(ctxs), R * Hkv, D, generator=g).to(torch.bfloat16)
+    pages = [-(-c // bs) for c in ctxs]
+    pool = sum(pages) + 3
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    bt = torch.full((len(ctxs), max(pages)), -1, dtype=torch.int32)
+    o = 0
+    for b, n in enumerate(pages):
+        bt[b, :n] = perm[o:o + n]
+        o += n
+    kv = gen.kv_values((2, pool, bs, Hkv, D), D, g, True, torch.float32)
+    factor = {"large": 300.0, "small": 1e-5, "mixed": 300.0}[case]
+    if case == "mixed":
+        for b, n in enumerate(pages):
+            for i in range(0, n, 2):
+                kv[1, int(bt[b, i])] *= factor
+    else:
+        kv[1] *= factor
+    kv = kv.to(torch.bfloat16)
+    codes, params = oc.int4_asym_compress(kv)
+    kv32 = oc.int4_asym_dequant_f32(*oc.int4_asym_quantize(kv))
+    s_v = oc.int4_asym_quantize(kv)[1][1].float()
+    if case == "small":
+        assert float(s_v.max()) < 2.0 ** -10
+    else:
+        assert float(s_v.max()) > 255.0
+    ctx = torch.tensor(ctxs, dtype=torch.int32)
+    got, flag = _run_decode(q, bt, ctx, pool, codes, params, Hkv, amf_hip.DECODE_MFMA)
+    assert flag == 0
+    ref = oatt.paged_decode_f64(q.float().numpy(), kv32[0].numpy(), kv32[1].numpy(), bt.numpy(),
+                                ctx.numpy())
+    check_attention(got / factor, ref / factor)
+
+
 @pytest.mark.parametrize("algo", [amf_hip.DECODE_MFMA, amf_hip.DECODE_VALU])
 def test_int4_paged_decode_ignores_slots_past_the_context(algo):
     """Slots past a sequence's context (the tail of its last page) may hold
