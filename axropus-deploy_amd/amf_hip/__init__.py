@@ -50,6 +50,7 @@ FMT_INT4_ASYM_G32 = 5
 DECODE_AUTO = 0
 DECODE_VALU = 1
 DECODE_MFMA = 2
+DECODE_MFMA_PRECISE = 3
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libamf_hip.so")
 

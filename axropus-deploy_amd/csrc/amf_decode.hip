@@ -76,6 +76,7 @@ struct DecodeArgs {
   int max_splits;
   int max_context_len;
   int head_fast;         // grid order, see work_head
+  int pv16;              // fp16 PV tiles where the V scales allow (else bf16 hi/lo throughout)
   float qk_scale_log2;  // softmax_scale * log2(e)
   float* ws;
   int32_t* err_flag;
@@ -687,7 +688,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     qk(c);
     u32x4 vc0, vc1, vp0, vp1;
     read_chunk_v(ring[c % D], lane, &vc0, &vc1, &vp0, &vp1);
-    if (!pv_f16_ok(vp0, vp1)) {
+    if (!a.pv16 || !pv_f16_ok(vp0, vp1)) {
       pending = true;
       break;
     }
@@ -1133,7 +1134,8 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
   if ((int64_t)max_context_len > (int64_t)block_table_stride * kBS)
     return fail(AMF_ERR_INVALID_ARG, "%s: max_context_len %d exceeds the block table (%d pages)",
                 who, max_context_len, block_table_stride);
-  if (algo != AMF_DECODE_AUTO && algo != AMF_DECODE_VALU && algo != AMF_DECODE_MFMA)
+  if (algo != AMF_DECODE_AUTO && algo != AMF_DECODE_VALU && algo != AMF_DECODE_MFMA &&
+      algo != AMF_DECODE_MFMA_PRECISE)
     return fail(AMF_ERR_INVALID_ARG, "%s: bad algo %d", who, algo);
   if (algo == AMF_DECODE_VALU && R > 4)
     return fail(AMF_ERR_UNSUPPORTED, "%s: the VALU path handles GQA groups up to 4", who);
@@ -1163,6 +1165,7 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
   a.head_fast = max_splits <= 65535;
   const float scale = softmax_scale > 0.0f ? softmax_scale : 1.0f / sqrtf((float)head_dim);
   a.qk_scale_log2 = scale * kLog2e;
+  a.pv16 = algo != AMF_DECODE_MFMA_PRECISE;
   a.ws = static_cast<float*>(workspace);
   a.err_flag = err_flag;
 

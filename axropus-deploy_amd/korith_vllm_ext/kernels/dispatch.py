@@ -195,7 +195,9 @@ def paged_int4_decode(q: torch.Tensor, kv: CompressedKV, block_tables: torch.Ten
     table's capacity, block_tables.shape[1] * 16, so no value is read back
     from the device.  `out` (contiguous [num_seqs, Hq, D] on the pool's
     device, bf16/fp16/fp32) and `workspace` (contiguous, on that device) are
-    checked before the launch; a bad one raises ValueError."""
+    checked before the launch; a bad one raises ValueError.  algo: "auto"
+    (= "mfma"), "mfma" (fp16 PV weights where a chunk's V scales allow),
+    "mfma_precise" (bf16 hi/lo PV weights throughout) or "valu"."""
     layout = kv.meta.get("_layout") if isinstance(kv, CompressedKV) else None
     if layout is None or kv.format != FMT_INT4_ASYM_G32 or layout.n_planes != 2:
         raise ValueError("paged decode needs the int4_asym_g32 CompressedKV of a layer page "
@@ -238,7 +240,8 @@ def paged_int4_decode(q: torch.Tensor, kv: CompressedKV, block_tables: torch.Ten
         _check_buffer(workspace, "workspace", dev)
     if workspace is None or workspace.numel() * workspace.element_size() < wsb:
         workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=dev)
-    algos = {"auto": amf_hip.DECODE_AUTO, "valu": amf_hip.DECODE_VALU, "mfma": amf_hip.DECODE_MFMA}
+    algos = {"auto": amf_hip.DECODE_AUTO, "valu": amf_hip.DECODE_VALU, "mfma": amf_hip.DECODE_MFMA,
+             "mfma_precise": amf_hip.DECODE_MFMA_PRECISE}
     amf_hip.call(
         "amf_int4_paged_decode_attn", q3.data_ptr(), amf_hip.dtype_tag(q3.dtype), out.data_ptr(),
         amf_hip.dtype_tag(out.dtype), blob.data_ptr() + layout.code_offset(0),

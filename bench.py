@@ -815,12 +815,14 @@ def long_context_70b(steps: int, warmup: int, cpu_jobs: list, want_cpu: bool) ->
     del case
     log("70b decode: building inputs")
     dc = DecodeCase(8, 64, 8, 131072, 131072, 6)
+    tp = time_launches(lambda: dc.launch(amf_hip_module().DECODE_MFMA_PRECISE), steps, warmup)
     td = time_launches(lambda: dc.launch(amf_hip_module().DECODE_MFMA), steps, warmup)
     msd = td.median_ms
     out["decode"] = td.leg(dc.algo_bytes, workload="decode_llama3_70b_b8_131k",
                            tok_per_s_per_layer=round(dc.batch / (msd * 1e-3), 1),
                            tok_per_s_model_80_layers=round(dc.batch / (80 * msd * 1e-3), 1),
-                           kv_tok_per_s=round(dc.sum_ctx / (msd * 1e-3), 1))
+                           kv_tok_per_s=round(dc.sum_ctx / (msd * 1e-3), 1),
+                           mfma_precise_median_ms=round(tp.median_ms, 5))
     log(f"70b decode: {out['decode']}")
     if want_cpu:
         cpu_jobs.append(("c5_llama3_70b", "cpu_decode_fallback", dc.cpu_fallback(1, 1, 1.0)))
@@ -1048,6 +1050,7 @@ def main() -> int:
         log("c4 int4 decode: building inputs")
         dc = DecodeCase()
         tv = time_launches(lambda: dc.launch(amf_hip.DECODE_VALU), args.steps, args.warmup)
+        tp = time_launches(lambda: dc.launch(amf_hip.DECODE_MFMA_PRECISE), args.steps, args.warmup)
         td = time_launches(lambda: dc.launch(amf_hip.DECODE_MFMA), args.steps, args.warmup)
         msd = td.median_ms
         result["c4_decode_llama3_8b"] = {"decode": td.leg(
@@ -1056,7 +1059,8 @@ def main() -> int:
             tok_per_s_model_32_layers=round(dc.batch / (32 * msd * 1e-3), 1),
             kv_tok_per_s=round(dc.sum_ctx / (msd * 1e-3), 1),
             valu_median_ms=round(tv.median_ms, 5),
-            mfma_over_valu_speedup=round(tv.median_ms / msd, 3))}
+            mfma_over_valu_speedup=round(tv.median_ms / msd, 3),
+            mfma_precise_median_ms=round(tp.median_ms, 5))}
         log(f"c4 decode: {result['c4_decode_llama3_8b']}")
         if want_cpu:
             cpu_jobs.append(("c4_decode_llama3_8b", "cpu_fallback", dc.cpu_fallback(4)))

@@ -259,7 +259,11 @@ int amf_int4_dequant_scatter(int32_t format,
  * device-to-host sync); a sequence with context 0 gets zeros.
  * softmax_scale <= 0 selects 1/sqrt(head_dim).
  * workspace: split-K partials, amf_int4_decode_workspace_bytes() bytes.
- * algo: AMF_DECODE_AUTO, AMF_DECODE_VALU or AMF_DECODE_MFMA.
+ * algo: AMF_DECODE_AUTO (= AMF_DECODE_MFMA), AMF_DECODE_VALU,
+ *       AMF_DECODE_MFMA (PV products on fp16 weights wherever a 32-token
+ *       chunk's V scales are 0 or in [2^-10, 255], bf16 hi/lo pairs
+ *       elsewhere) or AMF_DECODE_MFMA_PRECISE (bf16 hi/lo pairs throughout:
+ *       about 10x less PV rounding error, 7-12% slower).
  * Supported: head_dim 128, block_size 16, num_q_heads / num_kv_heads in
  * {1, 2, 4, 8}; anything else returns AMF_ERR_UNSUPPORTED.
  * Replaces int4_decode_attention (int4_decode_attention.py:6-9 ->
@@ -267,6 +271,7 @@ int amf_int4_dequant_scatter(int32_t format,
 #define AMF_DECODE_AUTO  0
 #define AMF_DECODE_VALU  1
 #define AMF_DECODE_MFMA  2
+#define AMF_DECODE_MFMA_PRECISE 3
 
 int64_t amf_int4_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
                                         int32_t num_kv_heads, int32_t head_dim,

@@ -74,7 +74,7 @@ def test_constants_match_header(lib):
     assert lib.amf_abi_version() == d["AMF_ABI_VERSION"] == amf_hip.ABI_VERSION
     for name in ("OK", "DTYPE_F16", "DTYPE_F32", "DTYPE_BF16", "FMT_FP8_E4M3", "FMT_FP8_E4M3_PH",
                  "FMT_INT4_SYM_BLOCK", "FMT_INT4_SYM", "FMT_INT4_ASYM_G32", "DECODE_AUTO",
-                 "DECODE_VALU", "DECODE_MFMA"):
+                 "DECODE_VALU", "DECODE_MFMA", "DECODE_MFMA_PRECISE"):
         assert getattr(amf_hip, name) == d["AMF_" + name], name
 
 

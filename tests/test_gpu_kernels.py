@@ -163,11 +163,13 @@ def test_fp8_tensor_format_bitexact(dtype, geom):
 
 # Scale groups of at least 4 MiB whose pages are whole multiples of 256
 # 16-byte chunks take the single-read cooperative kernel: an odd group count
-# (the last group has no partner buffer), one page per workgroup (CPT 8) and
-# several pages per workgroup (CPT 1).
+# (the last group has no partner buffer), one page per workgroup (CPT 8),
+# several pages per workgroup (CPT 1), and two pages per workgroup of CPT 8
+# (1200-page groups: more than the 768 workgroups that 256 CUs keep resident).
 COOP_CASES = [
     pytest.param(torch.bfloat16, dict(L=3, pool=512, n=160, bs=16, H=8, D=128), id="bf16-3groups"),
     pytest.param(torch.float16, dict(L=2, pool=2048, n=1200, bs=16, H=2, D=64), id="fp16-cpt1"),
+    pytest.param(torch.bfloat16, dict(L=2, pool=700, n=600, bs=16, H=8, D=128), id="bf16-2ppw"),
 ]
 
 
@@ -497,7 +499,10 @@ def _run_decode(q, bt, ctx, pool, codes, params, Hkv, algo, max_ctx=None,
     return out.float().cpu().numpy(), int(flag.item())
 
 
-@pytest.mark.parametrize("algo", [amf_hip.DECODE_MFMA, amf_hip.DECODE_VALU])
+DECODE_ALGOS = [amf_hip.DECODE_MFMA, amf_hip.DECODE_MFMA_PRECISE, amf_hip.DECODE_VALU]
+
+
+@pytest.mark.parametrize("algo", DECODE_ALGOS)
 @pytest.mark.parametrize("R", [1, 2, 4, 8])
 def test_int4_paged_decode_matches_f64(algo, R):
     if algo == amf_hip.DECODE_VALU and R > 4:
@@ -510,13 +515,17 @@ def test_int4_paged_decode_matches_f64(algo, R):
     ref = oatt.paged_decode_f64(q.float().numpy(), kv32[0].numpy(), kv32[1].numpy(), bt.numpy(),
                                 ctx.numpy())
     check_attention(got, ref)
+    if algo == amf_hip.DECODE_MFMA_PRECISE:
+        # bf16 hi + lo PV weights keep about 16 bits per weight (fp16
+        # weights: about 11 bits): mean error about 10x below the fp16 path's
+        check_attention(got, ref, max_abs=5e-3, mean_rel=2e-4)
     assert np.all(got[-1] == 0.0)                          # empty context -> zeros
     # bf16 output = round-to-nearest-even of the same fp32 result
     got16, _ = _run_decode(q, bt, ctx, pool, codes, params, Hkv, algo, out_dtype=torch.bfloat16)
     assert np.array_equal(got16, torch.from_numpy(got).to(torch.bfloat16).float().numpy())
 
 
-@pytest.mark.parametrize("algo", [amf_hip.DECODE_MFMA, amf_hip.DECODE_VALU])
+@pytest.mark.parametrize("algo", DECODE_ALGOS)
 def test_int4_paged_decode_peaked_scores(algo):
     """Extreme score range across tiles (after tests/test_kernels.py:115-133 of
     the reference): early tokens aligned with q dominate."""
@@ -538,8 +547,9 @@ def test_int4_paged_decode_peaked_scores(algo):
     check_attention(got, ref)
 
 
+@pytest.mark.parametrize("algo", [amf_hip.DECODE_MFMA, amf_hip.DECODE_MFMA_PRECISE])
 @pytest.mark.parametrize("case", ["large", "small", "mixed"])
-def test_int4_paged_decode_scale_range_paths(case):
+def test_int4_paged_decode_scale_range_paths(case, algo):
     """The MFMA kernel's PV product takes fp16 weights for a 32-token chunk
     whose V scales all lie in [2^-10, 255] and bf16 hi + lo weights otherwise.
     V scaled x300 (scales above 255), x1e-5 (below 2^-10), and x300 on every
@@ -574,14 +584,14 @@ def test_int4_paged_decode_scale_range_paths(case):
     else:
         assert float(s_v.max()) > 255.0
     ctx = torch.tensor(ctxs, dtype=torch.int32)
-    got, flag = _run_decode(q, bt, ctx, pool, codes, params, Hkv, amf_hip.DECODE_MFMA)
+    got, flag = _run_decode(q, bt, ctx, pool, codes, params, Hkv, algo)
     assert flag == 0
     ref = oatt.paged_decode_f64(q.float().numpy(), kv32[0].numpy(), kv32[1].numpy(), bt.numpy(),
                                 ctx.numpy())
     check_attention(got / factor, ref / factor)
 
 
-@pytest.mark.parametrize("algo", [amf_hip.DECODE_MFMA, amf_hip.DECODE_VALU])
+@pytest.mark.parametrize("algo", DECODE_ALGOS)
 def test_int4_paged_decode_ignores_slots_past_the_context(algo):
     """Slots past a sequence's context (the tail of its last page) may hold
     any bytes: NaN and infinite scales and zero points there must not reach
