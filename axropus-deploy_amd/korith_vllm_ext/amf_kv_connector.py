@@ -163,11 +163,13 @@ def _layer_index(layer_name: str) -> Optional[int]:
     return None
 
 
-def _layer_groups(layers: List[Tuple[int, str, torch.Tensor]]) -> List[list]:
-    """Split index-sorted (index, name, cache) layers into launch groups: the
-    first layer alone (the forward's first attention waits only for a short
-    launch), then runs of consecutive layers of one geometry in one launch
-    each.  A launch costs tens of microseconds of host work, more than the
+def _layer_groups(layers: List[Tuple[int, str, torch.Tensor]],
+                  split_first: bool) -> List[list]:
+    """Split index-sorted (index, name, cache) layers into launch groups: runs
+    of consecutive layers of one geometry in one launch each and, with
+    split_first (a restore on a side stream), the first layer alone before
+    them, so that the forward's first attention waits only for a short
+    launch.  A launch costs tens of microseconds of host work, more than the
     device time of a few layers, so the rest are not cut further: by the
     time the forward reaches the second layer the one large launch is well
     under way."""
@@ -177,7 +179,7 @@ def _layer_groups(layers: List[Tuple[int, str, torch.Tensor]]) -> List[list]:
         t = item[2]
         geom = (t.shape, t.stride(), t.dtype)
         g = groups[-1] if groups else None
-        if (g is not None and len(groups) > 1 and item[0] == g[-1][0] + 1
+        if (g is not None and (len(groups) > 1 or not split_first) and item[0] == g[-1][0] + 1
                 and geom == geom_prev):
             g.append(item)
         else:
@@ -243,7 +245,7 @@ class AMFKVConnector(KVConnectorBase_V1):
         self._bytes_per_layer = int(extra.get("bytes_per_layer", 1 << 23))
         self._default_format = str(extra.get("default_format", "fp8_e4m3"))
         self._min_prefix_tokens = int(extra.get("min_prefix_tokens", 64))
-        load_stream = str(extra.get("load_stream", "side")).lower()
+        load_stream = str(extra.get("load_stream", "current")).lower()
         if load_stream not in ("side", "current"):
             raise ValueError(f"load_stream must be 'side' or 'current', got {load_stream!r}")
         self._side_load = load_stream == "side"
@@ -396,7 +398,7 @@ class AMFKVConnector(KVConnectorBase_V1):
             if isinstance(kv, (list, tuple)):
                 kv = kv[ve] if len(kv) > ve else None
             items.append((name, kv))
-        key = tuple((name, id(kv)) for name, kv in items)
+        key = (self._side_load,) + tuple((name, id(kv)) for name, kv in items)
         memo = self._groups_memo
         if memo is not None and memo[0] == key and all(
                 r() is kv for r, (_, kv) in zip(memo[1], items)):
@@ -413,7 +415,7 @@ class AMFKVConnector(KVConnectorBase_V1):
                 continue
             layers.append((idx, name, pk))
         layers.sort(key=lambda t: t[0])
-        groups = _layer_groups(layers)
+        groups = _layer_groups(layers, self._side_load)
         refs = [weakref.ref(kv) if isinstance(kv, torch.Tensor) else (lambda: None)
                 for _, kv in items]
         self._groups_memo = (key, refs, groups)

@@ -436,10 +436,10 @@ class ConnectorCase:
         smeta = self.save_meta()
         save_ms = wall(lambda: self.save(smeta))
         lmeta = self.load_meta()
-        load_ms = wall(lambda: self.load(lmeta))
+        load_ms = wall(lambda: self.load(lmeta))      # the default: the forward's stream
         side = self.conn._side_load
-        self.conn._side_load = False
-        load_current_ms = wall(lambda: self.load(lmeta))
+        self.conn._side_load = True
+        load_side_ms = wall(lambda: self.load(lmeta))
         self.conn._side_load = side
         kernel_ms = time_launches(self.codec_launch(lmeta, "restore").launch, steps,
                                   warmup).median_ms
@@ -456,10 +456,10 @@ class ConnectorCase:
                 "load_ms": round(load_ms, 4), "load_GB/s": round(algo / load_ms / 1e6, 1),
                 "save_kernel_ms": round(save_kernel_ms, 4),
                 "save_over_kernel": round(save_ms / save_kernel_ms, 3),
-                "load_current_stream_ms": round(load_current_ms, 4),
+                "load_side_stream_ms": round(load_side_ms, 4),
                 "restore_kernel_ms": round(kernel_ms, 4),
                 "load_over_kernel": round(load_ms / kernel_ms, 3),
-                "load_current_stream_over_kernel": round(load_current_ms / kernel_ms, 3),
+                "load_side_stream_over_kernel": round(load_side_ms / kernel_ms, 3),
                 "slot_gather_unordered_ms": round(slot_ms, 4),
                 "slot_gather_GB/s": round(moved / slot_ms / 1e6, 1),
                 "slot_gather_frac": round(moved / slot_ms / 1e6 / HBM_PEAK_GBS, 4)}

@@ -165,6 +165,22 @@ def test_worker_without_gpu_is_inert():
 def test_bad_load_stream_option():
     with pytest.raises(ValueError):
         _conn(load_stream="sideways")
+    assert _conn()._side_load is False                  # the forward's stream by default
+    assert _conn(load_stream="side")._side_load is True
+
+
+def test_load_launch_groups():
+    """Consecutive layers of one geometry share a launch; on a side stream the
+    first layer is a launch of its own."""
+    from korith_vllm_ext.amf_kv_connector import _layer_groups
+
+    a = torch.zeros(2, 4, 16, 2, 64)
+    b = torch.zeros(2, 4, 16, 2, 128)
+    layers = [(i, f"l{i}", a) for i in range(4)] + [(4, "l4", b), (6, "l6", b), (7, "l7", b)]
+    ids = lambda groups: [[i for i, _, _ in g] for g in groups]
+    assert ids(_layer_groups(layers, False)) == [[0, 1, 2, 3], [4], [6, 7]]
+    assert ids(_layer_groups(layers, True)) == [[0], [1, 2, 3], [4], [6, 7]]
+    assert _layer_groups([], True) == []
 
 
 def test_token_pages_recut():
