@@ -175,6 +175,11 @@ __device__ __forceinline__ f32x4 mfma_f16(const u32x4& a, const u32x4& b, const 
 // order [t0 t4 t1 t5 t2 t6 t3 t7], as subnormals: even tokens c * 2^-24, odd
 // tokens 16 c * 2^-24 (the nibble left where it sits; the matching weights
 // carry 1/16).  Exact inputs, no bias term; five ops per 8 codes.
+// Nibble (dimension of the 8) held by operand element k of nib8_to_f16_sub,
+// and whether that element comes out x16 (a high nibble of its byte pair).
+__host__ __device__ constexpr int nib_of_k16(int k) { return (k >> 1) + 4 * (k & 1); }
+__host__ __device__ constexpr bool k16_x16(int k) { return (k & 2) != 0; }
+
 __device__ __forceinline__ u32x4 nib8_to_f16_sub(uint32_t w) {
   const uint32_t w8 = w >> 8;
   return u32x4{w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u};
@@ -387,11 +392,11 @@ __device__ __forceinline__ int work_split(const DecodeArgs& a) {
 #endif
 constexpr float kRescaleSlack = AMF_DECODE_RESCALE_SLACK;  // log2 units
 
-template <int R, bool QBF16>
+template <int R>
 __device__ __forceinline__ void chunk_qk(
-    const DecodeArgs& a, const uint8_t* slot, const bool (&pok)[2], int c0, int tok_end, int lo,
-    int hi, const u32x4 (&qa_hi)[(R + 3) / 4][4], const u32x4 (&qa_lo)[(R + 3) / 4][4],
-    const float (&qsum)[(R + 3) / 4][4], float (&m_run)[(R + 3) / 4], float (&l_run)[(R + 3) / 4],
+    const uint8_t* slot, const bool (&pok)[2], int c0, int tok_end, int lo, int hi,
+    const u32x4 (&qa)[(R + 3) / 4][4], float qk_scale, const float (&qsum)[(R + 3) / 4][4],
+    float (&m_run)[(R + 3) / 4], float (&l_run)[(R + 3) / 4],
     float (&corr)[(R + 3) / 4], f32x4 (&acc)[(R + 3) / 4][8],
     float (&p_lds)[(R + 3) / 4][2][4][16]) {
   constexpr int NT = (R + 3) / 4;
@@ -407,22 +412,19 @@ __device__ __forceinline__ void chunk_qk(
   for (int u = 0; u < 2; ++u) {
     u32x4 kb[4];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) kb[st] = nib8_to_bf16_128c(kcode[u][st]);
+    for (int st = 0; st < 4; ++st) kb[st] = nib8_to_f16_sub(kcode[u][st]);
     float ks[4], kz[4];
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
       ks[gi] = pscale(kpar[u][gi]);
-      kz[gi] = pzero(kpar[u][gi]) - kCodeBias * ks[gi];
+      kz[gi] = pzero(kpar[u][gi]);
     }
     const bool valid = pok[u] && (c0 + u * kBS + lo) < tok_end;
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
       f32x4 cacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        cacc = mfma_bf16(qa_hi[T][st], kb[st], cacc);
-        if constexpr (!QBF16) cacc = mfma_bf16(qa_lo[T][st], kb[st], cacc);
-      }
+      for (int st = 0; st < 4; ++st) cacc = mfma_f16(qa[T][st], kb[st], cacc);
       // One fma chain over the four groups (no zero seed: -0 + 0 would not fold).
       float sc = kz[0] * qsum[T][0];
       sc = __builtin_fmaf(ks[0], cacc[0], sc);
@@ -431,7 +433,7 @@ __device__ __forceinline__ void chunk_qk(
         sc = __builtin_fmaf(kz[gi], qsum[T][gi], sc);
         sc = __builtin_fmaf(ks[gi], cacc[gi], sc);
       }
-      x[T][u] = valid ? sc * a.qk_scale_log2 : -__builtin_inff();
+      x[T][u] = valid ? sc * qk_scale : -__builtin_inff();
     }
   }
 
@@ -598,7 +600,30 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
       qraw[T][st] = *reinterpret_cast<const u32x4*>(qr + 32 * hi + 8 * st);
     qraw[T][4] = *reinterpret_cast<const u32x4*>(qr + 32 * g + 8 * hi);
   }
-  u32x4 qa_hi[NT][4], qa_lo[NT][4];
+  // The QK^T tiles are fp16: K codes as exact subnormals c * 2^-24
+  // (nib8_to_f16_sub) against the query scaled by 2^-qe, qe chosen per wave
+  // so that its largest |q| lands in [2^14, 2^15): every bf16 or fp16 query
+  // element above 2^-24 of that maximum converts exactly.  The scores are
+  // then scaled back by 2^(24 + qe) (folded into qk_scale, and the zero-point
+  // sums qsum are scaled by 2^-(24 + qe) to match).
+  float qmax = 0.0f;
+#pragma unroll
+  for (int T = 0; T < NT; ++T)
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        qmax = fmaxf(qmax, fmaxf(fabsf(qval<QBF16>((uint16_t)(qraw[T][st][i] & 0xFFFFu))),
+                                 fabsf(qval<QBF16>((uint16_t)(qraw[T][st][i] >> 16)))));
+  qmax = wave_max_xor(qmax, 64);
+  // floor(log2(qmax)) - 14 for a normal finite qmax; 0 otherwise (a zero, a
+  // subnormal-only or a non-finite query keeps its own values)
+  const int qexp = (int)((f2u(qmax) >> 23) & 0xFFu);
+  const int qe = (qexp > 0 && qexp < 255) ? min(max(qexp - 127 - 14, -100), 100) : 0;
+  const float q_down = __builtin_ldexpf(1.0f, -qe);
+  const float qk_scale = a.qk_scale_log2 * __builtin_ldexpf(1.0f, 24 + qe);
+  const float qsum_down = __builtin_ldexpf(1.0f, -24 - qe);
+  u32x4 qa[NT][4];
   float qsum[NT][4];
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
@@ -608,25 +633,22 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     const bool mine = r < R && g == hi;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      // Elements in the k order of nib8_to_bf16_128c; an fp16 query is split
-      // into bf16 hi + lo (a bf16 query has lo = 0).
+      // Elements in the k order of nib8_to_f16_sub, the x16 ones divided by 16.
       const u32x4 raw = qraw[T][st];
       float xq[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        xq[2 * i] = qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu));
-        xq[2 * i + 1] = qval<QBF16>((uint16_t)(raw[i] >> 16));
+        xq[2 * i] = qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu)) * q_down;
+        xq[2 * i + 1] = qval<QBF16>((uint16_t)(raw[i] >> 16)) * q_down;
       }
-      u32x4 vh, vl;
+      u32x4 v;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint32_t h, l;
-        pk_bf16_hilo(xq[nib_of_k(2 * j)], xq[nib_of_k(2 * j + 1)], &h, &l);
-        vh[j] = mine ? h : 0u;
-        vl[j] = mine ? l : 0u;
+        const float e0 = xq[nib_of_k16(2 * j)] * (k16_x16(2 * j) ? 0.0625f : 1.0f);
+        const float e1 = xq[nib_of_k16(2 * j + 1)] * (k16_x16(2 * j + 1) ? 0.0625f : 1.0f);
+        v[j] = mine ? pk_f16(e0, e1) : 0u;
       }
-      qa_hi[T][st] = vh;
-      qa_lo[T][st] = vl;
+      qa[T][st] = v;
     }
     // Qsum[r][g] = sum of q[r][32 g .. 32 g + 31]: lanes (lo, hi) add 8 of
     // them, a cross-row sum completes it, then lane (t, j) fetches the four
@@ -640,7 +662,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     part += __shfl_xor(part, 16);
     part += __shfl_xor(part, 32);
 #pragma unroll
-    for (int gi = 0; gi < 4; ++gi) qsum[T][gi] = __shfl(part, 4 * hi + gi);
+    for (int gi = 0; gi < 4; ++gi) qsum[T][gi] = __shfl(part, 4 * hi + gi) * qsum_down;
   }
 
   float m_run[NT], l_run[NT], corr[NT];
@@ -678,8 +700,8 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     bool pok[2];
     split_page(spg, pi0 + 2 * c, &pok[0]);
     split_page(spg, pi0 + 2 * c + 1, &pok[1]);
-    chunk_qk<R, QBF16>(a, ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa_hi, qa_lo,
-                       qsum, m_run, l_run, corr, acc, p_lds);
+    chunk_qk<R>(ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa, qk_scale, qsum, m_run,
+                l_run, corr, acc, p_lds);
   };
   int c = 0;
   bool pending = false;  // chunk c has had QK^T and the softmax, not PV
