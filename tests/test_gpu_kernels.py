@@ -591,6 +591,23 @@ def test_int4_paged_decode_scale_range_paths(case, algo):
     check_attention(got / factor, ref / factor)
 
 
+@pytest.mark.parametrize("algo", [amf_hip.DECODE_MFMA, amf_hip.DECODE_MFMA_PRECISE])
+@pytest.mark.parametrize("factor", [3e5, 1e-6])
+def test_int4_paged_decode_query_range(factor, algo):
+    """The QK^T tiles take the query as fp16 scaled per wave by a power of two:
+    a bf16 query beyond the fp16 range (x3e5) and one far below its normal
+    range (x1e-6) must score as the float64 reference does."""
+    R, Hkv = 4, 2
+    q, bt, ctx, pool, codes, params, kv32 = _decode_case(R, Hkv, [40, 333, 1100], seed=151)
+    q = (q.float() * factor).to(torch.bfloat16)
+    assert (float(q.float().abs().max()) > 65504.0) == (factor > 1.0)
+    got, flag = _run_decode(q, bt, ctx, pool, codes, params, Hkv, algo)
+    assert flag == 0
+    ref = oatt.paged_decode_f64(q.float().numpy(), kv32[0].numpy(), kv32[1].numpy(), bt.numpy(),
+                                ctx.numpy())
+    check_attention(got, ref)
+
+
 @pytest.mark.parametrize("algo", DECODE_ALGOS)
 def test_int4_paged_decode_ignores_slots_past_the_context(algo):
     """Slots past a sequence's context (the tail of its last page) may hold
