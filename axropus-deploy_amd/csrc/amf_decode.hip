@@ -14,26 +14,33 @@
 // tokens (two 16-token pages), streamed through a small per-wave LDS ring by
 // non-temporal LDS DMA, and keeps, per query head of the GQA group, a
 // running max m (log2 domain), sum l and an unnormalised output.
-// A second kernel merges the splits.
+// A second kernel merges the splits.  (Merging inside this kernel, by the
+// last split of each (sequence, KV head) after an agent-scope ticket, needs an
+// agent-scope release per split, an L2 write-back on this chip: measured
+// 3.7x slower at batch 32 x 1K-32K contexts.)
 //
 // Dequantisation is folded into the dot products.  With K = s*c + z per
 // (token, 32-dim group):
 //   q.k = sum_g [ s_g * sum_{d in g} q_d c_d + z_g * sum_{d in g} q_d ].
-// Codes enter the matrix cores as the exact bf16 value 128 + c (the code as
-// the low mantissa byte of 128.0), so sum q_d (128 + c_d) - 128 sum q_d is
-// folded into the per-group constant: s * C + (z - 128 s) * Qsum.
+// Codes enter the matrix cores as exact fp16 subnormals c * 2^-24 (a nibble
+// masked in place; a high nibble comes out as 16 c * 2^-24 and the other
+// operand carries the 1/16), so no code bias enters the constant term.
 //
-// MFMA path (v_mfma_f32_16x16x32_bf16, 64 lanes, lane = 16 * hi + lo):
+// MFMA path (v_mfma_f32_16x16x32_f16, 64 lanes, lane = 16 * hi + lo):
 //  QK^T  computed as S^T[(r,g), t] = sum_k A[(r,g), k] B[k, t] where A holds
-//        q of head r restricted to group g (zero elsewhere: block structure)
-//        and B the 16 tokens' codes; four k-steps of 32 dims.  Lane (t = lo,
-//        j = hi) then owns C[(r = j, g = 0..3), t] and folds the four groups
-//        itself, so every output is useful.
-//  PV    O[(r,g), d] = sum_t W[(r,g), t] (128 + c_{t,d}) with W = p * s_g(t)
-//        split into bf16 hi + lo parts (two MFMAs, ~16-bit weights); the V
-//        pages are stored dim-major in 8x8 tiles, so a lane's B operand (8
-//        tokens of one dim) is one dword of a contiguous 32-byte run.  Only
-//        the row of each output column's own group is used.
+//        q of head r restricted to group g (zero elsewhere: block structure),
+//        as fp16 scaled per wave by a power of two, and B the 16 tokens'
+//        codes; four k-steps of 32 dims.  Lane (t = lo, j = hi) then owns
+//        C[(r = j, g = 0..3), t] and folds the four groups itself, so every
+//        output is useful.
+//  PV    O[(r,g), d] = sum_t W[(r,g), t] c_{t,d} with W = p * s_g(t) as one
+//        fp16 per weight where the chunk's V scales allow, otherwise (and for
+//        AMF_DECODE_MFMA_PRECISE) as a bf16 hi + lo pair against the codes as
+//        the exact bf16 128 + c (v_mfma_f32_16x16x32_bf16, the bias folded
+//        into the constant term); the V pages are stored dim-major in 8x8
+//        tiles, so a lane's B operand (8 tokens of one dim) is one dword of a
+//        contiguous 32-byte run.  Only the row of each output column's own
+//        group is used.
 // VALU path: the same data flow with fp32 FMAs (kept for the MFMA-vs-VALU
 // comparison and as a second implementation).
 #include <mutex>
