@@ -236,9 +236,15 @@ __global__ __launch_bounds__(kThreads) void int4_symblock_quant_looped_kernel(
   }
 }
 
-// INT4_SYM save, pass 1: per-channel absmax over a scale group.  Each
-// workgroup folds a strided set of pages into an LDS table, then issues one
-// global atomic max per channel into ws[group][head_dim].
+// INT4_SYM save, pass 1: per-channel absmax over a scale group.  One lane =
+// one 8-element chunk, as in pass 2 (kThreads * 8 is a multiple of head_dim,
+// so a lane's 8 channels stay fixed): every load instruction of a wave covers
+// 1 KiB of whole lines, and a page's chunks are all in flight at once.  Each
+// workgroup folds a strided set of pages, reduces the lanes that share
+// channels (shuffles, then an LDS table), and issues one global atomic max
+// per channel into ws[group][head_dim].
+constexpr int kAbsmaxUnroll = 8;
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void int4_channel_absmax_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
@@ -247,11 +253,10 @@ __global__ __launch_bounds__(kThreads) void int4_channel_absmax_kernel(
   const int plane = blockIdx.y;
   __shared__ uint32_t s_max[1024];
   for (int d = threadIdx.x; d < g.head_dim; d += kThreads) s_max[d] = 0;
-  __syncthreads();
-  const int col = sym_col(g), rpi = sym_rpi(g);
-  float m[32];
+  const int n8 = (int)((int64_t)g.n_rows * g.head_dim / 8);
+  float m[8];
 #pragma unroll
-  for (int q = 0; q < 32; ++q) m[q] = 0.0f;
+  for (int q = 0; q < 8; ++q) m[q] = 0.0f;
   for (int64_t j = blockIdx.x; j < n_pages; j += gridDim.x) {
     const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
     if (sp < 0 || sp >= pool) {
@@ -259,15 +264,34 @@ __global__ __launch_bounds__(kThreads) void int4_channel_absmax_kernel(
       continue;
     }
     const uint8_t* src = reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
-    for (int r = sym_row0(g); r < g.n_rows; r += rpi) {
-      float x[32];
-      load32<DT>(src + elem_bytes<DT>() * ((int64_t)r * g.head_dim + col * 32), x);
+    for (int base = threadIdx.x; base < n8; base += kThreads * kAbsmaxUnroll) {
+      float x[kAbsmaxUnroll][8];
 #pragma unroll
-      for (int q = 0; q < 32; ++q) m[q] = fmaxf(m[q], fabsf(x[q]));
+      for (int u = 0; u < kAbsmaxUnroll; ++u) {
+        const int k = base + u * kThreads;
+        if (k < n8) load8_stream<DT>(src + (int64_t)k * (8 * elem_bytes<DT>()), x[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kAbsmaxUnroll; ++u) {
+        if (base + u * kThreads < n8) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) m[q] = fmaxf(m[q], fabsf(x[u][q]));
+        }
+      }
     }
   }
+  // Lanes lane, lane + L, lane + 2L, ... of a wave (L = head_dim / 8 chunks
+  // per row) hold the same channels.
+  const int lpr = g.head_dim / 8;
 #pragma unroll
-  for (int q = 0; q < 32; ++q) atomicMax(&s_max[col * 32 + q], f2u(m[q]));
+  for (int q = 0; q < 8; ++q)
+    for (int o = 32; o >= lpr; o >>= 1) m[q] = fmaxf(m[q], __shfl_xor(m[q], o));
+  __syncthreads();  // s_max cleared
+  if ((threadIdx.x & 63) < lpr) {
+    const int d0 = (threadIdx.x * 8) % g.head_dim;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) atomicMax(&s_max[d0 + q], f2u(m[q]));
+  }
   __syncthreads();
   for (int d = threadIdx.x; d < g.head_dim; d += kThreads)
     atomicMax(ws + (int64_t)(plane / g.pps) * g.head_dim + d, s_max[d]);
@@ -283,15 +307,27 @@ __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
 // covers channels (8 k) % head_dim ..+7 and k advances by kThreads, a
 // multiple of head_dim / 8: a lane's 8 channels, and so its scales and
 // reciprocals, stay fixed for the whole page.
-constexpr int kChanUnroll = 4;
+#ifndef AMF_CHAN_UNROLL
+#define AMF_CHAN_UNROLL 4
+#endif
+constexpr int kChanUnroll = AMF_CHAN_UNROLL;
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void int4_channel_quant_gather_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
     const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
-    SymGeom g, const uint32_t* __restrict__ ws, int32_t* err_flag) {
+    const uint64_t* __restrict__ param_planes, SymGeom g, const uint32_t* __restrict__ ws,
+    int32_t* err_flag) {
   const int64_t j = blockIdx.x;
   const int plane = blockIdx.y;
+  // The group's fp16 scales (amf_codec.py:312-313), written once per group
+  // by its first plane's first page.
+  if (j == 0 && plane % g.pps == 0) {
+    _Float16* p = reinterpret_cast<_Float16*>(param_planes[plane]);
+    const uint32_t* gw = ws + (int64_t)(plane / g.pps) * g.head_dim;
+    for (int d = threadIdx.x; d < g.head_dim; d += kThreads)
+      p[d] = (_Float16)(fmaxf(u2f(gw[d]), 1e-8f) / kSymMax);
+  }
   const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
   if (sp < 0 || sp >= pool) {
     if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
@@ -316,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void int4_channel_quant_gather_kernel(
 #pragma unroll
     for (int u = 0; u < kChanUnroll; ++u) {
       const int k = base + u * kThreads;
-      if (k < n8) load8<DT>(src + (int64_t)k * (8 * elem_bytes<DT>()), x[u]);
+      if (k < n8) load8_stream<DT>(src + (int64_t)k * (8 * elem_bytes<DT>()), x[u]);
     }
 #pragma unroll
     for (int u = 0; u < kChanUnroll; ++u) {
@@ -332,17 +368,6 @@ __global__ __launch_bounds__(kThreads) void int4_channel_quant_gather_kernel(
         st_stream(w, codes + k);
       }
     }
-  }
-}
-
-__global__ void int4_channel_finalize_kernel(const uint64_t* __restrict__ param_planes,
-                                             const uint32_t* __restrict__ ws, int n_planes,
-                                             int pps, int head_dim) {
-  const int plane = blockIdx.y;
-  const int d = blockIdx.x * blockDim.x + threadIdx.x;
-  if (plane < n_planes && plane % pps == 0 && d < head_dim) {
-    _Float16* p = reinterpret_cast<_Float16*>(param_planes[plane]);
-    p[d] = (_Float16)(fmaxf(u2f(ws[(int64_t)(plane / pps) * head_dim + d]), 1e-8f) / kSymMax);
   }
 }
 
@@ -806,7 +831,7 @@ extern "C" int amf_int4_quant_gather(int32_t format, const uint64_t* cache_plane
 #undef AMF_LAUNCH
     return check_launch(who);
   }
-  // AMF_FMT_INT4_SYM: absmax pass, quant pass, fp16 scale finalize.
+  // AMF_FMT_INT4_SYM: absmax pass, then the quant pass (which also writes the fp16 scales).
   if (head_dim > 1024) return fail(AMF_ERR_UNSUPPORTED, "%s: head_dim > 1024", who);
   const int64_t need = amf_quant_workspace_bytes(format, n_planes, planes_per_scale, head_dim);
   if (!workspace || workspace_bytes < need)
@@ -814,14 +839,15 @@ extern "C" int amf_int4_quant_gather(int32_t format, const uint64_t* cache_plane
   uint32_t* ws = reinterpret_cast<uint32_t*>(workspace);
   const int64_t n_ws = need / 4;
   fill_u32_kernel<<<(unsigned)((n_ws + 255) / 256), 256, 0, s>>>(ws, n_ws, 0u);
-  dim3 rgrid((unsigned)(n_pages < 64 ? n_pages : 64), (unsigned)n_planes);
+#ifndef AMF_ABSMAX_WGS
+#define AMF_ABSMAX_WGS 64
+#endif
+  dim3 rgrid((unsigned)(n_pages < AMF_ABSMAX_WGS ? n_pages : AMF_ABSMAX_WGS), (unsigned)n_planes);
   AMF_WITH_DTYPE(cache_dtype, int4_channel_absmax_kernel<DT><<<rgrid, kThreads, 0, s>>>(
                                   cache_planes, cache_page_stride, block_ids, pool_pages, n_pages,
                                   g, ws, err_flag));
   AMF_WITH_DTYPE(cache_dtype, int4_channel_quant_gather_kernel<DT><<<grid, kThreads, 0, s>>>(
                                   cache_planes, cache_page_stride, block_ids, pool_pages,
-                                  code_planes, g, ws, err_flag));
-  dim3 fgrid((unsigned)((head_dim + 255) / 256), (unsigned)n_planes);
-  int4_channel_finalize_kernel<<<fgrid, 256, 0, s>>>(param_planes, ws, n_planes, g.pps, head_dim);
+                                  code_planes, param_planes, g, ws, err_flag));
   return check_launch(who);
 }

@@ -169,6 +169,24 @@ __device__ __forceinline__ void load8(const uint8_t* p, float* x) {
   }
 }
 
+// load8 for data read once (non-temporal loads where enabled): each load
+// instruction of a wave covers whole cache lines when lanes take consecutive
+// 8-element chunks.
+template <int DT>
+__device__ __forceinline__ void load8_stream(const uint8_t* p, float* x) {
+  if constexpr (DT == AMF_DTYPE_F32) {
+    const f32x4 a = ld_stream(reinterpret_cast<const f32x4*>(p));
+    const f32x4 b = ld_stream(reinterpret_cast<const f32x4*>(p) + 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = a[i];
+      x[4 + i] = b[i];
+    }
+  } else {
+    unpack8<DT == AMF_DTYPE_BF16>(ld_stream(reinterpret_cast<const u32x4*>(p)), x);
+  }
+}
+
 // fp32 -> eight cache elements at byte address p (streaming store; bf16/fp16
 // round to nearest even).
 template <int DT>

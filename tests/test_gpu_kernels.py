@@ -388,12 +388,15 @@ def test_int4_sym_channel_format_bitexact(dtype, geom):
 
 
 # Per-channel INT4 on larger scale groups (the reduction spans several
-# absmax workgroups per plane), head_dim 128, 64 and 256, with an
-# out-of-range block id.
+# absmax workgroups per plane), head_dim 64 to 1024, with an out-of-range
+# block id.
 CHAN_LARGE_CASES = [
     pytest.param(torch.bfloat16, dict(L=3, pool=512, n=160, bs=16, H=8, D=128), id="bf16-d128"),
     pytest.param(torch.float16, dict(L=2, pool=2048, n=1200, bs=16, H=2, D=64), id="fp16-d64"),
     pytest.param(torch.bfloat16, dict(L=2, pool=256, n=160, bs=16, H=4, D=256), id="bf16-d256"),
+    # rows of 64 and 128 lanes: no two lanes of a wave share channels
+    pytest.param(torch.float32, dict(L=2, pool=128, n=70, bs=16, H=2, D=512), id="fp32-d512"),
+    pytest.param(torch.float16, dict(L=2, pool=128, n=70, bs=16, H=1, D=1024), id="fp16-d1024"),
 ]
 
 
