@@ -428,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void fp8_ph_quant_gather_kernel(
     for (int i = 0; i < CPL; ++i) {
       const int c = lh + 32 * i;
       off[i] = ((int64_t)(c / cpr) * H + h) * D + (c % cpr) * 8;
-      load8<DT>(src + off[i] * elem_bytes<DT>(), x[i]);
+      load8_stream<DT>(src + off[i] * elem_bytes<DT>(), x[i]);
     }
     float m = 0.0f;
 #pragma unroll

@@ -109,8 +109,10 @@ __global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
 }
 
 // INT4_SYM_BLOCK save: page absmax -> scale -> codes; the page stays in
-// registers (R rows of 32 elements per lane).
-template <bool BF16, int R>
+// registers.  One lane = CPL 8-element chunks kThreads apart, so each load
+// instruction of a wave covers 1 KiB of whole lines (non-temporal: read once)
+// and each code store 256 contiguous bytes.
+template <bool BF16, int CPL>
 __global__ __launch_bounds__(kThreads) void int4_symblock_quant_gather_kernel(
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
     const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
@@ -122,30 +124,26 @@ __global__ __launch_bounds__(kThreads) void int4_symblock_quant_gather_kernel(
     if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
     return;
   }
-  const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
-  const uint8_t* __restrict__ src =
-      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
-  uint8_t* __restrict__ codes = reinterpret_cast<uint8_t*>(code_planes[plane]) + j * (page_elems / 2);
+  const int n8 = (int)((int64_t)g.n_rows * g.head_dim / 8);
+  const u32x4* __restrict__ src = reinterpret_cast<const u32x4*>(
+      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride);
+  uint32_t* __restrict__ codes = reinterpret_cast<uint32_t*>(code_planes[plane]) + j * n8;
   _Float16* __restrict__ params = reinterpret_cast<_Float16*>(param_planes[plane]);
-  const int col = sym_col(g), rpi = sym_rpi(g), r0 = sym_row0(g);
 
-  u32x4 v[R][4];
+  u32x4 v[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int k = threadIdx.x + i * kThreads;
+    if (k < n8) v[i] = ld_stream(src + k);
+  }
   float m = 0.0f;
 #pragma unroll
-  for (int k = 0; k < R; ++k) {
-    const int row = r0 + k * rpi;
-    if (row < g.n_rows) {
-      const u32x4* p =
-          reinterpret_cast<const u32x4*>(src + 2 * ((int64_t)row * g.head_dim + col * 32));
+  for (int i = 0; i < CPL; ++i) {
+    if (threadIdx.x + i * kThreads < n8) {
+      float x[8];
+      unpack8<BF16>(v[i], x);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) v[k][q] = p[q];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float x[8];
-        unpack8<BF16>(v[k][q], x);
-#pragma unroll
-        for (int n = 0; n < 8; ++n) m = fmaxf(m, fabsf(x[n]));
-      }
+      for (int n = 0; n < 8; ++n) m = fmaxf(m, fabsf(x[n]));
     }
   }
   m = wave_max_xor(m, 64);
@@ -160,25 +158,19 @@ __global__ __launch_bounds__(kThreads) void int4_symblock_quant_gather_kernel(
   const float rscale = 1.0f / scale;
   if (threadIdx.x == 0) params[j] = (_Float16)scale;
 #pragma unroll
-  for (int k = 0; k < R; ++k) {
-    const int row = r0 + k * rpi;
-    if (row < g.n_rows) {
-      u32x4 c;
+  for (int i = 0; i < CPL; ++i) {
+    const int k = threadIdx.x + i * kThreads;
+    if (k < n8) {
+      float x[8];
+      unpack8<BF16>(v[i], x);
+      uint32_t w = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float x[8];
-        unpack8<BF16>(v[k][q], x);
-        uint32_t w = 0;
-#pragma unroll
-        for (int n = 0; n < 8; ++n) {
-          float qv = __builtin_rintf(div_rn(x[n], scale, rscale));
-          qv = fminf(fmaxf(qv, -8.0f), 7.0f);
-          w |= (uint32_t)((int)qv + 8) << (4 * n);
-        }
-        c[q] = w;
+      for (int n = 0; n < 8; ++n) {
+        float qv = __builtin_rintf(div_rn(x[n], scale, rscale));
+        qv = fminf(fmaxf(qv, -8.0f), 7.0f);
+        w |= (uint32_t)((int)qv + 8) << (4 * n);
       }
-      st_stream(
-          c, reinterpret_cast<u32x4*>(codes + ((int64_t)row * g.head_dim + col * 32) / 2));
+      st_stream(w, codes + k);
     }
   }
 }
@@ -807,25 +799,27 @@ extern "C" int amf_int4_quant_gather(int32_t format, const uint64_t* cache_plane
   if ((rc = make_sym_geom(who, block_size, num_heads, head_dim, planes_per_scale, &g))) return rc;
   if (n_pages == 0) return ok();
   if (format == AMF_FMT_INT4_SYM_BLOCK) {
-    const int rpi = kThreads >> g.cpr_log2;
-    const int rows = (g.n_rows + rpi - 1) / rpi;
-    // Pages that fit lanes' registers take the single-read kernel; larger
-    // pages and fp32 caches the two-read one.
-    if (rows > 8 || cache_dtype == AMF_DTYPE_F32) {
+    const int64_t n8 = (int64_t)g.n_rows * g.head_dim / 8;
+    const int64_t cpl = (n8 + kThreads - 1) / kThreads;  // chunks per lane
+    // Pages that fit lanes' registers (up to 32 chunks of 8 elements per lane)
+    // take the single-read kernel; larger pages and fp32 caches the two-read one.
+    if (cpl > 32 || cache_dtype == AMF_DTYPE_F32) {
       AMF_WITH_DTYPE(cache_dtype, int4_symblock_quant_looped_kernel<DT><<<grid, kThreads, 0, s>>>(
                                       cache_planes, cache_page_stride, block_ids, pool_pages,
                                       code_planes, param_planes, g, err_flag));
       return check_launch(who);
     }
-#define AMF_LAUNCH(B, R)                                                                        \
-  int4_symblock_quant_gather_kernel<B, R><<<grid, kThreads, 0, s>>>(                            \
+#define AMF_LAUNCH(B, C)                                                                        \
+  int4_symblock_quant_gather_kernel<B, C><<<grid, kThreads, 0, s>>>(                            \
       cache_planes, cache_page_stride, block_ids, pool_pages, code_planes, param_planes, g, \
       err_flag)
 #define AMF_LAUNCH_R(B)                     \
-  if (rows <= 1) AMF_LAUNCH(B, 1);          \
-  else if (rows <= 2) AMF_LAUNCH(B, 2);     \
-  else if (rows <= 4) AMF_LAUNCH(B, 4);     \
-  else AMF_LAUNCH(B, 8)
+  if (cpl <= 1) AMF_LAUNCH(B, 1);           \
+  else if (cpl <= 2) AMF_LAUNCH(B, 2);      \
+  else if (cpl <= 4) AMF_LAUNCH(B, 4);      \
+  else if (cpl <= 8) AMF_LAUNCH(B, 8);      \
+  else if (cpl <= 16) AMF_LAUNCH(B, 16);    \
+  else AMF_LAUNCH(B, 32)
     if (bf16) { AMF_LAUNCH_R(true); } else { AMF_LAUNCH_R(false); }
 #undef AMF_LAUNCH_R
 #undef AMF_LAUNCH

@@ -914,9 +914,10 @@ def run_profile(name: str, steps: int, warmup: int) -> int:
         log(f"{name}: {t.leg(case.algo_bytes)}")
         return 0
     if name in ("fp8_restore", "int4_restore", "fp8_save", "int4_save", "fp8_tensor_save",
-                "int4_channel_save"):
+                "int4_channel_save", "int4_block_save", "int4_block_save"):
         fmt = ("fp8_e4m3" if name == "fp8_tensor_save" else
                "int4_sym" if name == "int4_channel_save" else
+               "int4_sym_block" if name == "int4_block_save" else
                "fp8_e4m3_ph" if name.startswith("fp8") else "int4_asym_g32")
         case = (RestoreCase(fmt, 32, 8, 128, 16384, 2048, 3) if fmt == "int4_asym_g32"
                 else RestoreCase(fmt, 32, 8, 128, 8192, 512, 2))
@@ -932,7 +933,7 @@ def run_profile(name: str, steps: int, warmup: int) -> int:
 
 
 PROFILES = ["fp8_restore", "int4_restore", "fp8_save", "int4_save", "fp8_tensor_save",
-            "int4_channel_save",
+            "int4_channel_save", "int4_block_save",
             "fp8_restore_70b", "decode_70b", "decode_mfma", "decode_valu", "copy", "slot_copy",
             "raw_gather", "raw_scatter", "page_scatter_8b", "page_scatter_8b_contig",
             "fp8_restore_contig"]
