@@ -583,7 +583,7 @@ __device__ __forceinline__ void asym_quant_v(const uint8_t* __restrict__ src,
 #pragma unroll
       for (int u = 0; u < kStageUnroll; ++u) {
         const int o = o0 + u * kThreads * 16;
-        if (o < page_bytes) v[u] = *reinterpret_cast<const u32x4*>(src + o);
+        if (o < page_bytes) v[u] = ld_stream(reinterpret_cast<const u32x4*>(src + o));
       }
 #pragma unroll
       for (int u = 0; u < kStageUnroll; ++u) {
@@ -658,10 +658,34 @@ __global__ __launch_bounds__(kThreads) void int4_asym_quant_gather_kernel(
       reinterpret_cast<uint8_t*>(code_planes[plane]) + j * (int64_t)H * g.hb_code_bytes;
   uint32_t* __restrict__ params =
       reinterpret_cast<uint32_t*>(param_planes[plane]) + j * (int64_t)H * g.hb_param_words;
-  if ((plane & 1) == 0)
-    asym_quant_k<DT>(src, codes, params, g);
-  else
+  if ((plane & 1) == 0) {
+    if (STAGED) {
+      // The page enters LDS by whole-line non-temporal loads (1 KiB per wave
+      // instruction); the items' 64-byte reads then come from LDS.  Reading
+      // the items straight from memory splits every line over four load
+      // instructions, which the non-temporal policy would fetch repeatedly.
+      const int page_bytes = 16 * H * g.head_dim * elem_bytes<DT>();
+      for (int o0 = threadIdx.x * 16; o0 < page_bytes; o0 += kThreads * 16 * kStageUnroll) {
+        u32x4 v[kStageUnroll];
+#pragma unroll
+        for (int u = 0; u < kStageUnroll; ++u) {
+          const int o = o0 + u * kThreads * 16;
+          if (o < page_bytes) v[u] = ld_stream(reinterpret_cast<const u32x4*>(src + o));
+        }
+#pragma unroll
+        for (int u = 0; u < kStageUnroll; ++u) {
+          const int o = o0 + u * kThreads * 16;
+          if (o < page_bytes) *reinterpret_cast<u32x4*>(lds + o) = v[u];
+        }
+      }
+      __syncthreads();
+      asym_quant_k<DT>(lds, codes, params, g);
+    } else {
+      asym_quant_k<DT>(src, codes, params, g);
+    }
+  } else {
     asym_quant_v<DT, STAGED>(src, codes, params, g, lds);
+  }
 }
 
 int check_int4_format(const char* who, int32_t format) {
