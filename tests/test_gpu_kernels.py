@@ -431,10 +431,17 @@ def test_int4_sym_channel_large_groups_bitexact(dtype, geom):
         assert torch.equal(sc.cpu(), scales), l
 
 
-@pytest.mark.parametrize("dtype,geom", CODEC_CASES)
+# Odd head counts (the V restore pairs head blocks) and head_dim 64 / 256.
+ASYM_CASES = CODEC_CASES + [
+    pytest.param(torch.bfloat16, dict(L=2, pool=32, n=12, bs=16, H=3, D=64), id="bf16-3heads-d64"),
+    pytest.param(torch.float16, dict(L=1, pool=32, n=10, bs=16, H=1, D=256), id="fp16-1head-d256"),
+]
+
+
+@pytest.mark.parametrize("dtype,geom", ASYM_CASES)
 def test_int4_asym_g32_format_bitexact(dtype, geom):
     values, src_ids, dst_ids = _codec_case(dtype, 50, geom)
-    values[0, 1, int(src_ids[2]), 4, 5, 32:64] = 1.5       # a constant group
+    values[0, 1, int(src_ids[2]), 4, geom["H"] - 1, 32:64] = 1.5   # a constant group
     layout, blobs, _ = _save("int4_asym_g32", values, src_ids, dtype, geom)
     want = []
     for l, blob in enumerate(blobs):
