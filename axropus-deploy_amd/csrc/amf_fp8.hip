@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void fp8_absmax_kernel(
 #pragma unroll
       for (int u = 0; u < kAbsUnroll; ++u) {
         const int k = base + u * kThreads;
-        if (k < n16) v[u] = src[k];
+        if (k < n16) v[u] = ld_stream(src + k);
       }
 #pragma unroll
       for (int u = 0; u < kAbsUnroll; ++u)
@@ -450,6 +450,47 @@ __global__ __launch_bounds__(kThreads) void fp8_ph_quant_gather_kernel(
       c[1] = f32x4_to_e4m3(x[i] + 4);
       st_stream(c, reinterpret_cast<u32x2*>(codes + off[i]));
     }
+  }
+}
+
+// Per-tensor save, pass 2 (after fp8_absmax_kernel): one lane = CPL
+// 8-element chunks kThreads apart, so each load instruction of a wave covers
+// 1 KiB of whole lines (non-temporal: read once) and each code store 512
+// contiguous bytes.  Same arithmetic as fp8_quant_gather_kernel<PER_TENSOR>.
+template <int DT, int CPL>
+__global__ __launch_bounds__(kThreads) void fp8_tensor_quant_kernel(
+    const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
+    const int32_t* __restrict__ block_ids, int64_t pool, const uint64_t* __restrict__ code_planes,
+    PageGeom g, const uint32_t* __restrict__ ws, int32_t* err_flag) {
+  const int64_t j = blockIdx.x;
+  const int plane = blockIdx.y;
+  const int64_t sp = block_ids ? (int64_t)block_ids[j] : j;
+  if (sp < 0 || sp >= pool) {
+    if (threadIdx.x == 0 && err_flag) atomicOr(err_flag, AMF_ERRFLAG_BLOCK_RANGE);
+    return;
+  }
+  const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
+  const uint8_t* __restrict__ src =
+      reinterpret_cast<const uint8_t*>(cache_planes[plane]) + sp * cache_stride;
+  u32x2* __restrict__ codes =
+      reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(code_planes[plane]) + j * page_elems);
+  float x[CPL][8];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i)
+    load8_stream<DT>(src + (int64_t)(threadIdx.x + i * kThreads) * (8 * elem_bytes<DT>()), x[i]);
+  const float a = fmaxf(u2f(ws[plane / g.pps]), tensor_floor<DT>());
+  // amf_codec.py:191 divides by max(scale, 1e-12); only a zero absmax (an
+  // fp16 cache, whose floor rounds to 0) reaches that clamp.
+  const float b = (a == 0.0f) ? 1e-12f : a / kFp8Max;
+  const float rb = 1.0f / b;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) x[i][q] = fminf(fmaxf(div_rn(x[i][q], b, rb), -kFp8Max), kFp8Max);
+    u32x2 c;
+    c[0] = f32x4_to_e4m3(x[i]);
+    c[1] = f32x4_to_e4m3(x[i] + 4);
+    st_stream(c, codes + threadIdx.x + i * kThreads);
   }
 }
 
@@ -799,6 +840,26 @@ extern "C" int amf_fp8_quant_gather(int32_t format, const uint64_t* cache_planes
                    fp8_absmax_kernel<DT><<<agrid, kThreads, 0, s>>>(
                        cache_planes, cache_page_stride, block_ids, pool_pages, n_pages, g, ws,
                        err_flag));
+  }
+  // Per-tensor pass 2: pages of 1-16 chunks of 8 elements per lane take the
+  // register-resident whole-line kernel.
+  const int64_t page_chunks = (int64_t)g.n_rows * head_dim / 8;
+  const int64_t tcpl = page_chunks % kThreads == 0 ? page_chunks / kThreads : 0;
+  if (pt && cache_dtype != AMF_DTYPE_F32 &&
+      (tcpl == 1 || tcpl == 2 || tcpl == 4 || tcpl == 8 || tcpl == 16)) {
+#define AMF_LAUNCH(C)                                                                          \
+  AMF_WITH_DTYPE(cache_dtype, fp8_tensor_quant_kernel<DT, C><<<grid, kThreads, 0, s>>>(        \
+                                  cache_planes, cache_page_stride, block_ids, pool_pages,      \
+                                  code_planes, g, ws, err_flag))
+    if (tcpl == 1) AMF_LAUNCH(1);
+    else if (tcpl == 2) AMF_LAUNCH(2);
+    else if (tcpl == 4) AMF_LAUNCH(4);
+    else if (tcpl == 8) AMF_LAUNCH(8);
+    else AMF_LAUNCH(16);
+#undef AMF_LAUNCH
+    AMF_WITH_DTYPE(cache_dtype, fp8_tensor_finalize_kernel<DT>
+                   <<<(n_planes + 255) / 256, 256, 0, s>>>(param_planes, ws, n_planes, g.pps));
+    return check_launch(who);
   }
   const int64_t head_chunks = (int64_t)(g.n_rows / g.num_heads) * head_dim / 8;
   const int cpl = (int)(head_chunks / 32);
