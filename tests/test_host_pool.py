@@ -135,3 +135,23 @@ def test_manager_restore_miss_paths(tmp_path):
     _write(mgr, toks, hdr + tab)
     assert mgr.restore_kv_state(toks, []) == 3 and mgr.stats()["hits"] == 1
     assert mgr.has_snapshot(toks) and not mgr.has_snapshot([1])
+
+
+@pytest.mark.parametrize("size", [1000, (8 << 20) + 12345, (21 << 20) + 7])
+@pytest.mark.parametrize("threads", ["1", "4"])
+def test_snapshot_file_io_round_trip(tmp_path, monkeypatch, size, threads):
+    """Chunked positional reads of a snapshot file (the AMFK tier's file
+    side) move exactly the file's bytes, with one thread or a pool, for sizes
+    below, at and past several chunks; a read past the end raises."""
+    from korith_vllm_ext import amf_kv_manager as m
+
+    monkeypatch.setenv("KORITH_AMF_IO_THREADS", threads)
+    data = np.random.default_rng(size).integers(0, 256, size, dtype=np.uint8)
+    path = tmp_path / "snap.kv"
+    data.tofile(path)
+    back = bytearray(size + 16)
+    with open(path, "rb") as f:
+        m._read_file_into(f.fileno(), memoryview(back), size)
+    assert np.array_equal(np.frombuffer(bytes(back[:size]), dtype=np.uint8), data)
+    with open(path, "rb") as f, pytest.raises(OSError):
+        m._read_file_into(f.fileno(), memoryview(bytearray(size + 100)), size + 100)
