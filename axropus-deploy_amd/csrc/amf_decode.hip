@@ -8,16 +8,19 @@
 // (batch, head), serial online softmax over 128-token tiles).  This kernel
 // adds paging (block tables), GQA and split-K.
 //
-// Work item: one wave per (sequence, KV head, split of split_tokens tokens);
-// grid = (num_kv_heads, max_splits, num_seqs), or (max_splits, num_kv_heads,
-// num_seqs) past 65535 splits.  The wave walks its split in chunks of 32
-// tokens (two 16-token pages), streamed through a small per-wave LDS ring by
-// non-temporal LDS DMA, and keeps, per query head of the GQA group, a
-// running max m (log2 domain), sum l and an unnormalised output.
-// A second kernel merges the splits.  (Merging inside this kernel, by the
-// last split of each (sequence, KV head) after an agent-scope ticket, needs an
-// agent-scope release per split, an L2 write-back on this chip: measured
-// 3.7x slower at batch 32 x 1K-32K contexts.)
+// Work (MFMA path, "stream-K"): the units (sequence, KV head, 32-token
+// chunk), sequence-major, are cut into G equal shares, G = the waves the
+// device keeps resident at once, one share per wave, so every wave streams
+// about the same number of chunks and the grid runs in one round whatever
+// the mix of context lengths.  A wave walks its share pair by pair; within a
+// (sequence, KV head) it streams chunks of 32 tokens (two 16-token pages)
+// through a small per-wave LDS ring by non-temporal LDS DMA, keeping per
+// query head of the GQA group a running max m (log2 domain), sum l and an
+// unnormalised output.  A pair held by one wave is finished in place; a pair
+// shared by several leaves one partial per wave (slot 0 of the wave for the
+// segment its share starts with, slot 1 for the one it ends with), and a
+// second kernel merges them with an LSE rescale.  The VALU path keeps fixed
+// splits of split_tokens tokens, one wave per (sequence, KV head, split).
 //
 // Dequantisation is folded into the dot products.  With K = s*c + z per
 // (token, 32-dim group):
@@ -43,6 +46,8 @@
 //        group is used.
 // VALU path: the same data flow with fp32 FMAs (kept for the MFMA-vs-VALU
 // comparison and as a second implementation).
+#include <algorithm>
+#include <map>
 #include <mutex>
 
 #include "amf_internal.h"
@@ -87,6 +92,10 @@ struct DecodeArgs {
   float qk_scale_log2;  // softmax_scale * log2(e)
   float* ws;
   int32_t* err_flag;
+  int out_dtype;
+  int num_seqs;
+  int stream_k;          // MFMA path: waves take equal shares of the (sequence, KV head, chunk) space
+  int sk_waves;          // grid size of the stream-K decode launch
 };
 
 // ---- lane helpers -----------------------------------------------------------
@@ -245,6 +254,93 @@ __device__ __forceinline__ int clamp_context(const DecodeArgs& a, int s) {
     ctx = ctx < 0 ? 0 : max_tok;
   }
   return ctx;
+}
+
+// ---- stream-K work map (MFMA path) ----------------------------------------
+// Units are (sequence, KV head, 32-token chunk), sequence-major; wave w of G
+// takes units [w C / G, (w + 1) C / G) of the C in all.  A (sequence, KV head)
+// spanned by several waves is merged from their partials: slot 0 of a wave
+// holds the segment its share starts with, slot 1 the one it ends with.
+
+// Chunks of sequence s (its context clamped as clamp_context does).
+__device__ __forceinline__ int64_t sk_chunks(const DecodeArgs& a, int s) {
+  int ctx = a.context_lens[s];
+  const int max_tok = min(a.bt_stride * kBS, a.max_context_len);
+  ctx = ctx < 0 ? 0 : min(ctx, max_tok);
+  return (ctx + 31) / 32;
+}
+
+// A wave-uniform value the compiler cannot prove uniform, moved to SGPRs.
+__device__ __forceinline__ int64_t uni64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int uni32(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// C: units of all sequences (every lane gets it).
+__device__ __forceinline__ int64_t sk_total_units(const DecodeArgs& a, int n_seqs) {
+  const int lane = threadIdx.x & 63;
+  int64_t t = 0;
+  for (int i = lane; i < n_seqs; i += 64) t += sk_chunks(a, i);
+  return uni64(wave_sum_i64(t) * a.num_kv_heads);
+}
+
+// Sequence s holding unit u0 < C, and the units P before it.
+__device__ __forceinline__ void sk_locate(const DecodeArgs& a, int n_seqs, int64_t u0, int* s_out,
+                                          int64_t* p_out) {
+  const int lane = threadIdx.x & 63;
+  int64_t before = 0;
+  for (int s0 = 0; s0 < n_seqs; s0 += 64) {
+    const int64_t n = s0 + lane < n_seqs ? sk_chunks(a, s0 + lane) * a.num_kv_heads : 0;
+    int64_t incl = n;  // inclusive prefix over the lanes
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    const uint64_t hit = __ballot(before + incl > u0);
+    if (hit) {
+      const int l = __builtin_ctzll(hit);
+      *s_out = uni32(s0 + l);
+      *p_out = uni64(before + __shfl(incl - n, l));
+      return;
+    }
+    before = uni64(before + __shfl(incl, 63));
+  }
+  *s_out = n_seqs;
+  *p_out = before;
+}
+
+// Wave holding unit u: the largest w with w C / G <= u.
+__device__ __forceinline__ int64_t sk_wave_of(int64_t u, int64_t total, int64_t G) {
+  return ((u + 1) * G - 1) / total;
+}
+
+// 8 output elements at element offset `row` of the output, in its dtype.
+__device__ __forceinline__ void store_out8(const DecodeArgs& a, int64_t row, const float* y) {
+  if (a.out_dtype == AMF_DTYPE_F32) {
+    float* out = static_cast<float*>(a.out) + row;
+    *reinterpret_cast<float4*>(out) = float4{y[0], y[1], y[2], y[3]};
+    *reinterpret_cast<float4*>(out + 4) = float4{y[4], y[5], y[6], y[7]};
+  } else {
+    uint16_t* out = static_cast<uint16_t*>(a.out) + row;
+    u32x4 v;
+    if (a.out_dtype == AMF_DTYPE_BF16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[i] = (uint32_t)oval<true>(y[2 * i]) | ((uint32_t)oval<true>(y[2 * i + 1]) << 16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[i] = (uint32_t)oval<false>(y[2 * i]) | ((uint32_t)oval<false>(y[2 * i + 1]) << 16);
+    }
+    *reinterpret_cast<u32x4*>(out) = v;
+  }
 }
 
 // Physical page of logical page `pi` (which must lie inside the context);
@@ -571,6 +667,9 @@ __device__ __forceinline__ void chunk_pv(const u32x4& vc0, const u32x4& vc1, con
 #ifndef AMF_DECODE_WAVES_PER_EU
 #define AMF_DECODE_WAVES_PER_EU 2
 #endif
+#ifndef AMF_DECODE_WAVES_PER_EU_SMALL_GQA
+#define AMF_DECODE_WAVES_PER_EU_SMALL_GQA 3
+#endif
 
 // D: chunks in the LDS ring (D - 1 in flight while one computes).
 #ifndef AMF_DECODE_RING_SMALL_GQA
@@ -580,187 +679,232 @@ __device__ __forceinline__ void chunk_pv(const u32x4& vc0, const u32x4& vc1, con
 #define AMF_DECODE_RING_GQA8 3
 #endif
 template <int R, bool QBF16, int D = (R > 4 ? AMF_DECODE_RING_GQA8 : AMF_DECODE_RING_SMALL_GQA)>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(AMF_DECODE_WAVES_PER_EU)))
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
+    R > 4 ? AMF_DECODE_WAVES_PER_EU : AMF_DECODE_WAVES_PER_EU_SMALL_GQA)))
 void int4_decode_mfma_kernel(DecodeArgs a) {
   constexpr int NT = (R + 3) / 4;  // 16-row tiles of (head, group) pairs
-  const int sp = work_split(a), h = work_head(a), s = blockIdx.z;
   const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
-  const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
-  const int bt_raw = split_table_entry(a, bt, sp);
-  const int ctx = clamp_context(a, s);
-  const int tok_begin = sp * a.split_tokens;
-  if (tok_begin >= ctx) return;
-  const int tok_end = min(ctx, tok_begin + a.split_tokens);
-  const uint16_t* qh = a.q + ((int64_t)s * a.num_q_heads + (int64_t)h * R) * kD;
-
-  // ---- Q operands (constant for the wave) ----
-  // Every lane loads (rows past the GQA group clamped to its last row) and
-  // the lanes a value does not belong to zero it afterwards: loads under a
-  // lane condition would each wait for the one before.
-  u32x4 qraw[NT][5];
-#pragma unroll
-  for (int T = 0; T < NT; ++T) {
-    const int r = 4 * T + (lo >> 2), g = lo & 3;
-    const uint16_t* qr = qh + (r < R ? r : R - 1) * kD;
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-      qraw[T][st] = *reinterpret_cast<const u32x4*>(qr + 32 * hi + 8 * st);
-    qraw[T][4] = *reinterpret_cast<const u32x4*>(qr + 32 * g + 8 * hi);
-  }
-  // The QK^T tiles are fp16: K codes as exact subnormals c * 2^-24
-  // (nib8_to_f16_sub) against the query scaled by 2^-qe, qe chosen per wave
-  // so that its largest |q| lands in [2^14, 2^15): every bf16 or fp16 query
-  // element above 2^-24 of that maximum converts exactly.  The scores are
-  // then scaled back by 2^(24 + qe) (folded into qk_scale, and the zero-point
-  // sums qsum are scaled by 2^-(24 + qe) to match).
-  float qmax = 0.0f;
-#pragma unroll
-  for (int T = 0; T < NT; ++T)
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        qmax = fmaxf(qmax, fmaxf(fabsf(qval<QBF16>((uint16_t)(qraw[T][st][i] & 0xFFFFu))),
-                                 fabsf(qval<QBF16>((uint16_t)(qraw[T][st][i] >> 16)))));
-  qmax = wave_max_xor(qmax, 64);
-  // floor(log2(qmax)) - 14 for a normal finite qmax; 0 otherwise (a zero, a
-  // subnormal-only or a non-finite query keeps its own values)
-  const int qexp = (int)((f2u(qmax) >> 23) & 0xFFu);
-  const int qe = (qexp > 0 && qexp < 255) ? min(max(qexp - 127 - 14, -100), 100) : 0;
-  const float q_down = __builtin_ldexpf(1.0f, -qe);
-  const float qk_scale = a.qk_scale_log2 * __builtin_ldexpf(1.0f, 24 + qe);
-  const float qsum_down = __builtin_ldexpf(1.0f, -24 - qe);
-  u32x4 qa[NT][4];
-  float qsum[NT][4];
-#pragma unroll
-  for (int T = 0; T < NT; ++T) {
-    const int r = 4 * T + (lo >> 2), g = lo & 3;
-    // A operand of k-step st: row (r, g) holds q[r][32 g + 8 st + e] on the
-    // lanes whose k-slice (hi) is group g.
-    const bool mine = r < R && g == hi;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      // Elements in the k order of nib8_to_f16_sub, the x16 ones divided by 16.
-      const u32x4 raw = qraw[T][st];
-      float xq[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        xq[2 * i] = qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu)) * q_down;
-        xq[2 * i + 1] = qval<QBF16>((uint16_t)(raw[i] >> 16)) * q_down;
-      }
-      u32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float e0 = xq[nib_of_k16(2 * j)] * (k16_x16(2 * j) ? 0.0625f : 1.0f);
-        const float e1 = xq[nib_of_k16(2 * j + 1)] * (k16_x16(2 * j + 1) ? 0.0625f : 1.0f);
-        v[j] = mine ? pk_f16(e0, e1) : 0u;
-      }
-      qa[T][st] = v;
-    }
-    // Qsum[r][g] = sum of q[r][32 g .. 32 g + 31]: lanes (lo, hi) add 8 of
-    // them, a cross-row sum completes it, then lane (t, j) fetches the four
-    // groups of head 4T + j.
-    float part = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      part += qval<QBF16>((uint16_t)(qraw[T][4][i] & 0xFFFFu)) +
-              qval<QBF16>((uint16_t)(qraw[T][4][i] >> 16));
-    part = r < R ? part : 0.0f;
-    part += __shfl_xor(part, 16);
-    part += __shfl_xor(part, 32);
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) qsum[T][gi] = __shfl(part, 4 * hi + gi) * qsum_down;
-  }
-
-  float m_run[NT], l_run[NT], corr[NT];
-  f32x4 acc[NT][8];
-#pragma unroll
-  for (int T = 0; T < NT; ++T) {
-    m_run[T] = kNegBig;
-    l_run[T] = 0.0f;
-    corr[T] = 0.0f;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) acc[T][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
+  const int H = a.num_kv_heads;
   __shared__ __attribute__((aligned(16))) float p_lds[NT][2][4][16];
-
-  // Ring pipeline: chunks c + 1 .. c + D - 1 are in flight while chunk c
-  // computes.
   __shared__ __attribute__((aligned(16))) uint8_t ring[D][kSlotBytes];
-  const SplitPages spg = split_pages(a, bt_raw, tok_begin, tok_end);
-  const int nch = (tok_end - tok_begin + 31) / 32;
-  const int pi0 = tok_begin / kBS;
-  auto issue = [&](int c) {
-    bool ok;
-    const int64_t p0 = split_page(spg, pi0 + 2 * c, &ok);
-    const int64_t p1 = split_page(spg, pi0 + 2 * c + 1, &ok);
-    dma_chunk(a, p0, p1, h, lane, ring[c % D]);
-  };
-#pragma unroll
-  for (int k = 0; k + 1 < D; ++k)
-    if (k < nch) issue(k);
-  // Chunks take the fp16 PV path until one whose V scales it cannot take;
-  // from that chunk on the split finishes on the bf16 path (a second loop, so
-  // that each loop keeps its own register footprint).
-  auto qk = [&](int c) {
-    dma_wait<D>(min(D - 1, nch - 1 - c));
-    bool pok[2];
-    split_page(spg, pi0 + 2 * c, &pok[0]);
-    split_page(spg, pi0 + 2 * c + 1, &pok[1]);
-    chunk_qk<R>(ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa, qk_scale, qsum, m_run,
-                l_run, corr, acc, p_lds);
-  };
-  int c = 0;
-  bool pending = false;  // chunk c has had QK^T and the softmax, not PV
-  for (; c < nch; ++c) {
-    if (c + D - 1 < nch) issue(c + D - 1);
-    qk(c);
-    u32x4 vc0, vc1, vp0, vp1;
-    read_chunk_v(ring[c % D], lane, &vc0, &vc1, &vp0, &vp1);
-    if (!a.pv16 || !pv_f16_ok(vp0, vp1)) {
-      pending = true;
-      break;
-    }
-    chunk_pv<R, true>(vc0, vc1, vp0, vp1, lo, hi, corr, acc, p_lds);
-  }
-  for (; c < nch; ++c) {
-    if (!pending) {
-      if (c + D - 1 < nch) issue(c + D - 1);
-      qk(c);
-    }
-    pending = false;
-    u32x4 vc0, vc1, vp0, vp1;
-    read_chunk_v(ring[c % D], lane, &vc0, &vc1, &vp0, &vp1);
-    chunk_pv<R, false>(vc0, vc1, vp0, vp1, lo, hi, corr, acc, p_lds);
-  }
 
-  // ---- write the split's partial (unnormalised O, m, l) ----
-#pragma unroll
-  for (int T = 0; T < NT; ++T) {
-    const float l_tot = row_sum16(l_run[T]);
-    float cf = corr[T];
-    cf += __shfl_xor(cf, 16);
-    cf += __shfl_xor(cf, 32);
-    const int gsel = lo >> 2;  // group of dims 8 lo .. 8 lo + 7
-    const float cv = __shfl(cf, 4 * hi + gsel);
-    const int r = 4 * T + hi;
-    if (r < R) {
-      float o[8];
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const f32x4 t = acc[T][b];
-        const float v = gsel == 0 ? t[0] : gsel == 1 ? t[1] : gsel == 2 ? t[2] : t[3];
-        o[b] = __builtin_fmaf(v, 1.0f / kPvScale, cv);
+  // ---- this wave's share: units (sequence, KV head, 32-token chunk) in that
+  // order, units [w C / G, (w + 1) C / G) for wave w of G ----
+  const int64_t total = sk_total_units(a, a.num_seqs);
+  // G <= C: every wave of the first G gets at least one unit, so the waves
+  // spanning a pair all hold a part of it (the rest exit).
+  const int64_t G = min((int64_t)a.sk_waves, total), w = blockIdx.x;
+  if (w >= G) return;
+  const int64_t u0 = uni64(w * total / G), u1 = uni64((w + 1) * total / G);
+  if (u0 >= u1) return;
+  int s = 0;
+  int64_t P = 0;  // units before sequence s
+  sk_locate(a, a.num_seqs, u0, &s, &P);
+  int64_t u = u0;
+  while (u < u1) {
+    const int ctx = uni32(clamp_context(a, s));
+    const int nch_s = (ctx + 31) / 32;
+    if (u >= P + (int64_t)H * nch_s) {  // past this sequence (or an empty one)
+      P += (int64_t)H * nch_s;
+      ++s;
+      continue;
+    }
+    const int h = uni32((int)((u - P) / nch_s));
+    const int64_t pair0 = uni64(P + (int64_t)h * nch_s), pair1 = pair0 + nch_s;
+    const int64_t seg_end = uni64(min(u1, pair1));
+    const int c_a = uni32((int)(u - pair0)), c_b = uni32((int)(seg_end - pair0));
+    const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
+    const uint16_t* qh = a.q + ((int64_t)s * a.num_q_heads + (int64_t)h * R) * kD;
+
+    // ---- Q operands (constant for the wave) ----
+    // Every lane loads (rows past the GQA group clamped to its last row) and
+    // the lanes a value does not belong to zero it afterwards: loads under a
+    // lane condition would each wait for the one before.
+    u32x4 qraw[NT][5];
+  #pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const int r = 4 * T + (lo >> 2), g = lo & 3;
+      const uint16_t* qr = qh + (r < R ? r : R - 1) * kD;
+  #pragma unroll
+      for (int st = 0; st < 4; ++st)
+        qraw[T][st] = *reinterpret_cast<const u32x4*>(qr + 32 * hi + 8 * st);
+      qraw[T][4] = *reinterpret_cast<const u32x4*>(qr + 32 * g + 8 * hi);
+    }
+    // The QK^T tiles are fp16: K codes as exact subnormals c * 2^-24
+    // (nib8_to_f16_sub) against the query scaled by 2^-qe, qe chosen per wave
+    // so that its largest |q| lands in [2^14, 2^15): every bf16 or fp16 query
+    // element above 2^-24 of that maximum converts exactly.  The scores are
+    // then scaled back by 2^(24 + qe) (folded into qk_scale, and the zero-point
+    // sums qsum are scaled by 2^-(24 + qe) to match).
+    float qmax = 0.0f;
+  #pragma unroll
+    for (int T = 0; T < NT; ++T)
+  #pragma unroll
+      for (int st = 0; st < 4; ++st)
+  #pragma unroll
+        for (int i = 0; i < 4; ++i)
+          qmax = fmaxf(qmax, fmaxf(fabsf(qval<QBF16>((uint16_t)(qraw[T][st][i] & 0xFFFFu))),
+                                   fabsf(qval<QBF16>((uint16_t)(qraw[T][st][i] >> 16)))));
+    qmax = wave_max_xor(qmax, 64);
+    // floor(log2(qmax)) - 14 for a normal finite qmax; 0 otherwise (a zero, a
+    // subnormal-only or a non-finite query keeps its own values)
+    const int qexp = (int)((f2u(qmax) >> 23) & 0xFFu);
+    const int qe = (qexp > 0 && qexp < 255) ? min(max(qexp - 127 - 14, -100), 100) : 0;
+    const float q_down = __builtin_ldexpf(1.0f, -qe);
+    const float qk_scale = a.qk_scale_log2 * __builtin_ldexpf(1.0f, 24 + qe);
+    const float qsum_down = __builtin_ldexpf(1.0f, -24 - qe);
+    u32x4 qa[NT][4];
+    float qsum[NT][4];
+  #pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const int r = 4 * T + (lo >> 2), g = lo & 3;
+      // A operand of k-step st: row (r, g) holds q[r][32 g + 8 st + e] on the
+      // lanes whose k-slice (hi) is group g.
+      const bool mine = r < R && g == hi;
+  #pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        // Elements in the k order of nib8_to_f16_sub, the x16 ones divided by 16.
+        const u32x4 raw = qraw[T][st];
+        float xq[8];
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          xq[2 * i] = qval<QBF16>((uint16_t)(raw[i] & 0xFFFFu)) * q_down;
+          xq[2 * i + 1] = qval<QBF16>((uint16_t)(raw[i] >> 16)) * q_down;
+        }
+        u32x4 v;
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e0 = xq[nib_of_k16(2 * j)] * (k16_x16(2 * j) ? 0.0625f : 1.0f);
+          const float e1 = xq[nib_of_k16(2 * j + 1)] * (k16_x16(2 * j + 1) ? 0.0625f : 1.0f);
+          v[j] = mine ? pk_f16(e0, e1) : 0u;
+        }
+        qa[T][st] = v;
       }
-      float* base = a.ws + (((int64_t)s * a.num_q_heads + (int64_t)h * R + r) * a.max_splits + sp) *
-                               kPartStride;
-      *reinterpret_cast<float4*>(base + 8 * lo) = float4{o[0], o[1], o[2], o[3]};
-      *reinterpret_cast<float4*>(base + 8 * lo + 4) = float4{o[4], o[5], o[6], o[7]};
-      if (lo == 0) {
-        base[kD] = m_run[T];
-        base[kD + 1] = l_tot;
+      // Qsum[r][g] = sum of q[r][32 g .. 32 g + 31]: lanes (lo, hi) add 8 of
+      // them, a cross-row sum completes it, then lane (t, j) fetches the four
+      // groups of head 4T + j.
+      float part = 0.0f;
+  #pragma unroll
+      for (int i = 0; i < 4; ++i)
+        part += qval<QBF16>((uint16_t)(qraw[T][4][i] & 0xFFFFu)) +
+                qval<QBF16>((uint16_t)(qraw[T][4][i] >> 16));
+      part = r < R ? part : 0.0f;
+      part += __shfl_xor(part, 16);
+      part += __shfl_xor(part, 32);
+  #pragma unroll
+      for (int gi = 0; gi < 4; ++gi) qsum[T][gi] = __shfl(part, 4 * hi + gi) * qsum_down;
+    }
+
+
+    float m_run[NT], l_run[NT], corr[NT];
+    f32x4 acc[NT][8];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      m_run[T] = kNegBig;
+      l_run[T] = 0.0f;
+      corr[T] = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) acc[T][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    // Pieces of at most 32 chunks (64 pages: one block-table entry per lane).
+    for (int pc = c_a; pc < c_b; pc += 32) {
+      const int tok_begin = pc * 32;
+      const int tok_end = min(ctx, min(c_b, pc + 32) * 32);
+      const int pfirst = tok_begin / kBS, pn = (tok_end - tok_begin + kBS - 1) / kBS;
+      const int bt_raw = (lane < pn && pfirst + lane < a.bt_stride) ? bt[pfirst + lane] : -1;
+      // Ring pipeline: chunks c + 1 .. c + D - 1 are in flight while chunk c
+      // computes.
+      const SplitPages spg = split_pages(a, bt_raw, tok_begin, tok_end);
+      const int nch = (tok_end - tok_begin + 31) / 32;
+      const int pi0 = tok_begin / kBS;
+      auto issue = [&](int c) {
+        bool ok;
+        const int64_t p0 = split_page(spg, pi0 + 2 * c, &ok);
+        const int64_t p1 = split_page(spg, pi0 + 2 * c + 1, &ok);
+        dma_chunk(a, p0, p1, h, lane, ring[c % D]);
+      };
+    #pragma unroll
+      for (int k = 0; k + 1 < D; ++k)
+        if (k < nch) issue(k);
+      // Chunks take the fp16 PV path until one whose V scales it cannot take;
+      // from that chunk on the split finishes on the bf16 path (a second loop, so
+      // that each loop keeps its own register footprint).
+      auto qk = [&](int c) {
+        dma_wait<D>(min(D - 1, nch - 1 - c));
+        bool pok[2];
+        split_page(spg, pi0 + 2 * c, &pok[0]);
+        split_page(spg, pi0 + 2 * c + 1, &pok[1]);
+        chunk_qk<R>(ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa, qk_scale, qsum, m_run,
+                    l_run, corr, acc, p_lds);
+      };
+      int c = 0;
+      bool pending = false;  // chunk c has had QK^T and the softmax, not PV
+      for (; c < nch; ++c) {
+        if (c + D - 1 < nch) issue(c + D - 1);
+        qk(c);
+        u32x4 vc0, vc1, vp0, vp1;
+        read_chunk_v(ring[c % D], lane, &vc0, &vc1, &vp0, &vp1);
+        if (!a.pv16 || !pv_f16_ok(vp0, vp1)) {
+          pending = true;
+          break;
+        }
+        chunk_pv<R, true>(vc0, vc1, vp0, vp1, lo, hi, corr, acc, p_lds);
+      }
+      for (; c < nch; ++c) {
+        if (!pending) {
+          if (c + D - 1 < nch) issue(c + D - 1);
+          qk(c);
+        }
+        pending = false;
+        u32x4 vc0, vc1, vp0, vp1;
+        read_chunk_v(ring[c % D], lane, &vc0, &vc1, &vp0, &vp1);
+        chunk_pv<R, false>(vc0, vc1, vp0, vp1, lo, hi, corr, acc, p_lds);
+      }
+
+    }
+
+    // ---- the segment's result: the output itself when the wave holds the
+    // whole (sequence, KV head), else a partial (unnormalised O, m, l) in
+    // its slot: 0 for the share's first segment, 1 for its last ----
+    const bool owned = c_a == 0 && c_b == nch_s;
+    const int slot = u == u0 ? 0 : 1;
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const float l_tot = row_sum16(l_run[T]);
+      float cf = corr[T];
+      cf += __shfl_xor(cf, 16);
+      cf += __shfl_xor(cf, 32);
+      const int gsel = lo >> 2;  // group of dims 8 lo .. 8 lo + 7
+      const float cv = __shfl(cf, 4 * hi + gsel);
+      const int r = 4 * T + hi;
+      if (r < R) {
+        float o[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const f32x4 t = acc[T][b];
+          const float v = gsel == 0 ? t[0] : gsel == 1 ? t[1] : gsel == 2 ? t[2] : t[3];
+          o[b] = __builtin_fmaf(v, 1.0f / kPvScale, cv);
+        }
+        if (owned) {
+          // as the merge does for one split: its weight exp2(m - m) = 1
+          const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+          const int64_t row = ((int64_t)s * a.num_q_heads + (int64_t)h * R + r) * kD + 8 * lo;
+          float y[8];
+#pragma unroll
+          for (int b = 0; b < 8; ++b) y[b] = o[b] * inv;
+          store_out8(a, row, y);
+        } else {
+          float* base = a.ws + ((w * 2 + slot) * R + r) * kPartStride;
+          *reinterpret_cast<float4*>(base + 8 * lo) = float4{o[0], o[1], o[2], o[3]};
+          *reinterpret_cast<float4*>(base + 8 * lo + 4) = float4{o[4], o[5], o[6], o[7]};
+          if (lo == 0) {
+            base[kD] = m_run[T];
+            base[kD + 1] = l_tot;
+          }
+        }
       }
     }
+    u = seg_end;
   }
 }
 
@@ -939,8 +1083,53 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int half = lane >> 5, c = lane & 31;
   const int ctx = clamp_context(a, s);
-  const int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
+  int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
   const float* base = a.ws + ((int64_t)s * a.num_q_heads + qhd) * a.max_splits * kPartStride;
+  // Stream-K decode: the parts of (s, KV head) are the slots of waves wf..wl
+  // (the first one's slot 1 when its share began in an earlier pair).
+  const int R = a.num_q_heads / a.num_kv_heads;
+  int64_t wf = 0;
+  bool first_slot1 = false;
+  if (a.stream_k) {
+    const int64_t nch = sk_chunks(a, s);
+    n_sp = 0;
+    if (nch > 0) {
+      int64_t t_all = 0, t_before = 0;
+      for (int i = tid; i < a.num_seqs; i += kMergeThreads) {
+        const int64_t c = sk_chunks(a, i);
+        t_all += c;
+        t_before += i < s ? c : 0;
+      }
+      t_all = wave_sum_i64(t_all);
+      t_before = wave_sum_i64(t_before);
+      __shared__ int64_t s_cnt[2][kMergeWaves];
+      if (lane == 0) {
+        s_cnt[0][w] = t_all;
+        s_cnt[1][w] = t_before;
+      }
+      __syncthreads();
+      t_all = 0;
+      t_before = 0;
+#pragma unroll
+      for (int i = 0; i < kMergeWaves; ++i) {
+        t_all += s_cnt[0][i];
+        t_before += s_cnt[1][i];
+      }
+      const int64_t H = a.num_kv_heads, total = t_all * H;
+      const int64_t G = min((int64_t)a.sk_waves, total);  // as the decode launch uses it
+      const int64_t pair0 = t_before * H + (int64_t)(qhd / R) * nch;
+      wf = sk_wave_of(pair0, total, G);
+      const int64_t wl = sk_wave_of(pair0 + nch - 1, total, G);
+      if (wf == wl) return;  // one wave held the whole pair and wrote the output
+      n_sp = (int)(wl - wf + 1);
+      first_slot1 = wf * total / G < pair0;
+    }
+  }
+  auto part = [&](int k) -> const float* {
+    if (!a.stream_k) return base + (int64_t)k * kPartStride;
+    const int64_t slot = (k == 0 && first_slot1) ? 1 : 0;
+    return a.ws + (((wf + k) * 2 + slot) * R + qhd % R) * kPartStride;
+  };
   // The accumulators of this thread's first kMergePre splits are loaded
   // together with the (m, l) words, before the maximum is known, so the merge
   // waits on memory once (rows clamped into the sequence's splits; a clamped
@@ -950,17 +1139,17 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
 #pragma unroll
   for (int j = 0; j < kMergePre; ++j) {
     const int k = max(min(k_first + 2 * kMergeWaves * j, n_sp - 1), 0);
-    pre[j] = *reinterpret_cast<const float4*>(base + (int64_t)k * kPartStride + 4 * c);
+    pre[j] = *reinterpret_cast<const float4*>(part(k) + 4 * c);
   }
   float m0 = kNegBig, l0 = 0.0f;  // (m, l) of split tid, kept for the weights
   if (tid < n_sp) {
-    const float2 ml = *reinterpret_cast<const float2*>(base + (int64_t)tid * kPartStride + kD);
+    const float2 ml = *reinterpret_cast<const float2*>(part(tid) + kD);
     m0 = ml.x;
     l0 = ml.y;
   }
   float M = m0;
   for (int i = tid + kMergeThreads; i < n_sp; i += kMergeThreads)
-    M = fmaxf(M, base[(int64_t)i * kPartStride + kD]);
+    M = fmaxf(M, part(i)[kD]);
   M = wave_max_xor(M, 64);
   if (lane == 0) sred[w] = M;
   __syncthreads();
@@ -976,7 +1165,7 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
     if (i < n_sp) {
       float mi = m0, li = l0;
       if (i0 != 0) {
-        const float2 ml = *reinterpret_cast<const float2*>(base + (int64_t)i * kPartStride + kD);
+        const float2 ml = *reinterpret_cast<const float2*>(part(i) + kD);
         mi = ml.x;
         li = ml.y;
       }
@@ -1005,7 +1194,7 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
     for (int k = k_from; k < cnt; k += 2 * kMergeWaves) {
       const float wk = wgt[k];
       const float4 v =
-          *reinterpret_cast<const float4*>(base + (int64_t)(i0 + k) * kPartStride + 4 * c);
+          *reinterpret_cast<const float4*>(part(i0 + k) + 4 * c);
       o.x += wk * v.x;
       o.y += wk * v.y;
       o.z += wk * v.z;
@@ -1115,6 +1304,43 @@ void* scratch_address(const char* who) {
   return g_scratch_ptr[dev];
 }
 
+// Waves of one stream-K decode launch: as many as the device keeps resident
+// at once (occupancy of the kernel x compute units), the larger of the bf16-
+// and fp16-query kernels of the group size; 0 when the runtime cannot say.
+template <int R>
+int sk_waves_for() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int ncu = 0;
+  if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      ncu <= 0)
+    return 0;
+  int best = 0;
+  for (const void* fn : {reinterpret_cast<const void*>(&int4_decode_mfma_kernel<R, true>),
+                         reinterpret_cast<const void*>(&int4_decode_mfma_kernel<R, false>)}) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, 64, 0) != hipSuccess) return 0;
+    best = std::max(best, nb);
+  }
+  const int g = std::max(1, best) * ncu;
+  cache[dev] = g;
+  return g;
+}
+
+int sk_waves(int R) {
+  switch (R) {
+    case 1: return sk_waves_for<1>();
+    case 2: return sk_waves_for<2>();
+    case 4: return sk_waves_for<4>();
+    default: return sk_waves_for<8>();
+  }
+}
+
 }  // namespace
 
 extern "C" int64_t amf_int4_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
@@ -1123,9 +1349,18 @@ extern "C" int64_t amf_int4_decode_workspace_bytes(int32_t num_seqs, int32_t num
   if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim != kD) return 0;
   const int split = choose_split(num_seqs, num_kv_heads, max_context_len);
   const int64_t max_splits = (max_context_len + split - 1) / split;
-  return (int64_t)num_seqs * num_q_heads * (max_splits > 0 ? max_splits : 1) * kPartStride *
-         (int64_t)sizeof(float);
+  // split partials of the VALU path; two partial slots per wave of the MFMA path
+  const int64_t split_bytes = (int64_t)num_seqs * num_q_heads * (max_splits > 0 ? max_splits : 1) *
+                              kPartStride * (int64_t)sizeof(float);
+  const int R = num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 ? num_q_heads / num_kv_heads
+                                                                     : 1;
+  const int64_t sk_bytes =
+      (R == 1 || R == 2 || R == 4 || R == 8)
+          ? (int64_t)sk_waves(R) * 2 * R * kPartStride * (int64_t)sizeof(float)
+          : 0;
+  return std::max(split_bytes, sk_bytes);
 }
+
 
 extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* out,
                                           int32_t out_dtype,
@@ -1197,6 +1432,17 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
   a.pv16 = algo != AMF_DECODE_MFMA_PRECISE;
   a.ws = static_cast<float*>(workspace);
   a.err_flag = err_flag;
+  a.out_dtype = out_dtype;
+  a.num_seqs = num_seqs;
+  a.stream_k = algo != AMF_DECODE_VALU;
+  a.sk_waves = a.stream_k ? sk_waves(R) : 0;
+  if (a.stream_k && a.sk_waves <= 0)
+    return fail(AMF_ERR_RUNTIME, "%s: could not size the decode grid (device occupancy query)", who);
+  // Stream-K unit arithmetic stays in int64: units x waves < 2^62.
+  if (a.stream_k && ((int64_t)max_context_len / 32 + 1) * num_seqs * num_kv_heads >
+                        ((int64_t)1 << 62) / a.sk_waves)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: %d sequences x %d KV heads x %d tokens is too large", who,
+                num_seqs, num_kv_heads, max_context_len);
 
   hipStream_t st = as_stream(stream);
   const bool bf16 = q_dtype == AMF_DTYPE_BF16;
@@ -1213,6 +1459,8 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
       else if (R == 2) { AMF_LAUNCH_B(int4_decode_valu_kernel, 2); }
       else { AMF_LAUNCH_B(int4_decode_valu_kernel, 4); }
     } else {
+#undef AMF_LAUNCH
+#define AMF_LAUNCH(K, RR, B) K<RR, B><<<dim3((unsigned)a.sk_waves), 64, 0, st>>>(a)
       if (R == 1) { AMF_LAUNCH_B(int4_decode_mfma_kernel, 1); }
       else if (R == 2) { AMF_LAUNCH_B(int4_decode_mfma_kernel, 2); }
       else if (R == 4) { AMF_LAUNCH_B(int4_decode_mfma_kernel, 4); }

@@ -535,6 +535,25 @@ def test_int4_paged_decode_matches_f64(algo, R):
     assert np.array_equal(got16, torch.from_numpy(got).to(torch.bfloat16).float().numpy())
 
 
+def test_int4_paged_decode_shares_span_many_pairs():
+    """Many short sequences (more chunks than the device has resident waves):
+    a wave's share then covers several (sequence, KV head) pairs, the middle
+    ones whole (finished in place) and the ends shared with neighbours
+    (merged from partial slots); empty sequences in between give zeros."""
+    g = torch.Generator().manual_seed(91)
+    ctxs = torch.randint(1, 160, (700,), generator=g).tolist()
+    for i in range(0, 700, 97):
+        ctxs[i] = 0
+    R, Hkv = 4, 8
+    q, bt, ctx, pool, codes, params, kv32 = _decode_case(R, Hkv, ctxs, seed=92)
+    got, flag = _run_decode(q, bt, ctx, pool, codes, params, Hkv, amf_hip.DECODE_MFMA)
+    assert flag == 0
+    ref = oatt.paged_decode_f64(q.float().numpy(), kv32[0].numpy(), kv32[1].numpy(), bt.numpy(),
+                                ctx.numpy())
+    check_attention(got, ref)
+    assert np.all(got[np.asarray(ctxs) == 0] == 0.0)
+
+
 @pytest.mark.parametrize("algo", DECODE_ALGOS)
 def test_int4_paged_decode_peaked_scores(algo):
     """Extreme score range across tiles (after tests/test_kernels.py:115-133 of
