@@ -258,7 +258,9 @@ int amf_int4_dequant_scatter(int32_t format,
  * max_context_len bounds every context_lens[i] (it sizes the grid: no
  * device-to-host sync); a sequence with context 0 gets zeros.
  * softmax_scale <= 0 selects 1/sqrt(head_dim).
- * workspace: split-K partials, amf_int4_decode_workspace_bytes() bytes.
+ * workspace: split partials, amf_int4_decode_workspace_bytes() bytes (it
+ *              sizes the MFMA path for the current device's resident waves:
+ *              call it with the device of the launch current).
  * algo: AMF_DECODE_AUTO (= AMF_DECODE_MFMA), AMF_DECODE_VALU,
  *       AMF_DECODE_MFMA (PV products on fp16 weights wherever a 32-token
  *       chunk's V scales are 0 or in [2^-10, 255], bf16 hi/lo pairs
