@@ -37,13 +37,14 @@
 //        C[(r = j, g = 0..3), t] and folds the four groups itself, so every
 //        output is useful.
 //  PV    O[(r,g), d] = sum_t W[(r,g), t] c_{t,d} with W = p * s_g(t) as one
-//        fp16 per weight where the chunk's V scales allow, otherwise (and for
-//        AMF_DECODE_MFMA_PRECISE) as a bf16 hi + lo pair against the codes as
-//        the exact bf16 128 + c (v_mfma_f32_16x16x32_bf16, the bias folded
-//        into the constant term); the V pages are stored dim-major in 8x8
-//        tiles, so a lane's B operand (8 tokens of one dim) is one dword of a
-//        contiguous 32-byte run.  Only the row of each output column's own
-//        group is used.
+//        fp16 per weight where an error budget on the rounding of those
+//        weights and the chunk's V scales allow (pv_single_ok), otherwise
+//        (and for AMF_DECODE_MFMA_PRECISE) as a bf16 hi + lo pair against the
+//        codes as the exact bf16 128 + c (v_mfma_f32_16x16x32_bf16, the bias
+//        folded into the constant term); the V pages are stored dim-major in
+//        8x8 tiles, so a lane's B operand (8 tokens of one dim) is one dword
+//        of a contiguous 32-byte run.  Only the row of each output column's
+//        own group is used.
 // VALU path: the same data flow with fp32 FMAs (kept for the MFMA-vs-VALU
 // comparison and as a second implementation).
 #include <algorithm>
@@ -136,11 +137,12 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // element order is k = [n0 n2 n4 n6 n1 n3 n5 n7] (kNibOfK below); the other
 // operand of the product is laid out in the same order.
 constexpr float kCodeBias = 128.0f;
-// The PV accumulators hold O * kPvScale (fp16 subnormal codes are c * 2^-24).
-constexpr float kPvScale = 0x1p-24f;
+// The PV accumulators hold O * kPvScale: fp16 subnormal codes are c * 2^-24
+// (x16 for odd tokens) against fp16 weights 16 w (w for odd tokens).
+constexpr float kPvScale = 0x1p-20f;
 // fp16 bit patterns bounding the V scales of the fp16 PV path: [2^-10, 255].
 constexpr uint32_t kF16ScaleMinBits = 0x1400u;  // 2^-10
-constexpr uint32_t kF16ScaleMaxBits = 0x5BF8u;  // 255
+constexpr uint32_t kF16ScaleMaxBits = 0x4BC0u;  // 15.5
 
 __device__ __forceinline__ u32x4 nib8_to_bf16_128c(uint32_t w) {
   const uint32_t ev = w & 0x0F0F0F0Fu;          // bytes: n0 n2 n4 n6
@@ -363,7 +365,7 @@ __device__ __forceinline__ int64_t page_of(const DecodeArgs& a, const int32_t* b
 // ([4096, 5120)).  Each block arrives by one LDS DMA (global_load_lds_dwordx4,
 // non-temporal: every line is read once, by one instruction); DMA lane L
 // writes slot bytes [16 L, 16 L + 16), and its source address is chosen so
-// that the compute lanes' reads (read_chunk_k, read_chunk_v) are consecutive 16-byte slots
+// that the compute lanes' reads (read_chunk_k, read_chunk_vc/vp) are consecutive 16-byte slots
 // (no bank conflicts).  No load registers are held while a chunk is in
 // flight, so a wave keeps several chunks in flight at any occupancy.
 constexpr int kSlotBytes = 5120;
@@ -407,12 +409,17 @@ __device__ __forceinline__ void read_chunk_k(const uint8_t* slot, int lane, u32x
   kpar[1] = *reinterpret_cast<const u32x4*>(slot + 4096 + 256 + lo * 16);
 }
 
-__device__ __forceinline__ void read_chunk_v(const uint8_t* slot, int lane, u32x4* vc0,
-                                             u32x4* vc1, u32x4* vp0, u32x4* vp1) {
+__device__ __forceinline__ void read_chunk_vc(const uint8_t* slot, int lane, u32x4* vc0,
+                                              u32x4* vc1) {
   const int lo = lane & 15, hi = lane >> 4;
   const uint8_t* vs = slot + 2048 + 1024 * (hi >> 1) + (lo + 16 * (hi & 1)) * 16;
   *vc0 = *reinterpret_cast<const u32x4*>(vs);
   *vc1 = *reinterpret_cast<const u32x4*>(vs + 512);
+}
+
+__device__ __forceinline__ void read_chunk_vp(const uint8_t* slot, int lane, u32x4* vp0,
+                                              u32x4* vp1) {
+  const int lo = lane & 15, hi = lane >> 4;
   const uint8_t* ps = slot + 4096 + 512 + 256 * (hi >> 1) + ((lo & 3) * 16 + 8 * (hi & 1)) * 4;
   *vp0 = *reinterpret_cast<const u32x4*>(ps);
   *vp1 = *reinterpret_cast<const u32x4*>(ps + 16);
@@ -498,10 +505,10 @@ constexpr float kRescaleSlack = AMF_DECODE_RESCALE_SLACK;  // log2 units
 template <int R>
 __device__ __forceinline__ void chunk_qk(
     const uint8_t* slot, const bool (&pok)[2], int c0, int tok_end, int lo, int hi,
-    const u32x4 (&qa)[(R + 3) / 4][4], float qk_scale, const float (&qsum)[(R + 3) / 4][4],
+    const u32x4 (&qa)[(R + 3) / 4][4], float qk_scale, const float (&qs_lds)[(R + 3) / 4][4][4],
     float (&m_run)[(R + 3) / 4], float (&l_run)[(R + 3) / 4],
-    float (&corr)[(R + 3) / 4], f32x4 (&acc)[(R + 3) / 4][8],
-    float (&p_lds)[(R + 3) / 4][2][4][16]) {
+    float (&corr)[(R + 3) / 4], float (&wsum)[(R + 3) / 4], float (&lb)[(R + 3) / 4],
+    f32x4 (&acc)[(R + 3) / 4][8], float (&p_lds)[(R + 3) / 4][2][4][16]) {
   constexpr int NT = (R + 3) / 4;
   const int lane = lo + 16 * hi;
   // K operands only; the V side is read from the slot just before the PV
@@ -525,15 +532,18 @@ __device__ __forceinline__ void chunk_qk(
     const bool valid = pok[u] && (c0 + u * kBS + lo) < tok_end;
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
+      // the group sums of head 4T + hi's query (one LDS broadcast read)
+      const float4 q4 = *reinterpret_cast<const float4*>(&qs_lds[T][hi][0]);
+      const float qsum[4] = {q4.x, q4.y, q4.z, q4.w};
       f32x4 cacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int st = 0; st < 4; ++st) cacc = mfma_f16(qa[T][st], kb[st], cacc);
       // One fma chain over the four groups (no zero seed: -0 + 0 would not fold).
-      float sc = kz[0] * qsum[T][0];
+      float sc = kz[0] * qsum[0];
       sc = __builtin_fmaf(ks[0], cacc[0], sc);
 #pragma unroll
       for (int gi = 1; gi < 4; ++gi) {
-        sc = __builtin_fmaf(kz[gi], qsum[T][gi], sc);
+        sc = __builtin_fmaf(kz[gi], qsum[gi], sc);
         sc = __builtin_fmaf(ks[gi], cacc[gi], sc);
       }
       x[T][u] = valid ? sc * qk_scale : -__builtin_inff();
@@ -556,8 +566,11 @@ __device__ __forceinline__ void chunk_qk(
       l_run[T] *= alpha;
 #pragma unroll
       for (int b = 0; b < 8; ++b) acc[T][b] *= alpha;
-      // corr lives in the A layout: lane lo holds head 4T + lo/4.
-      corr[T] *= __shfl(alpha, 16 * (lo >> 2));
+      // corr, wsum and lb live in the A layout: lane lo holds head 4T + lo/4.
+      const float alpha_a = __shfl(alpha, 16 * (lo >> 2));
+      corr[T] *= alpha_a;
+      wsum[T] *= alpha_a;
+      lb[T] *= alpha_a;
       m_run[T] = m_new;
     }
     p[T][0] = exp2_fast(x[T][0] - m_run[T]);
@@ -569,95 +582,246 @@ __device__ __forceinline__ void chunk_qk(
   __builtin_amdgcn_wave_barrier();
 }
 
-// Whether a chunk's V scales allow the fp16 PV path (see chunk_pv): each lane
-// checks the scale words of its 8 tokens, then the wave votes.
-__device__ __forceinline__ bool pv_f16_ok(const u32x4& vp0, const u32x4& vp1) {
+// ---- PV product: weights, the choice of their form ----
+//
+// The PV product is a 16x16x32 tile of weights (rows: head x group, k:
+// tokens) times codes (k: tokens, columns: dims).  Codes 0-15 are exact in
+// either input type; the weight w = p * s (p <= 2^8 after the lazy rescale,
+// s the token's V scale of the row's group) is the rounded part.  All forms
+// accumulate O * 2^-20 (restored by the partial write), so chunks of any
+// form can share a split.
+//  fp16: one fp16 per weight (relative error <= 2^-11), 16 w for even and w
+//   for odd tokens against the codes as exact fp16 subnormals (c * 2^-24,
+//   16 c * 2^-24 for odd tokens, see nib8_to_f16_sub); one MFMA per tile.
+//  fp16 pair: the same operand plus a second, fp16 (x - hi) (about 22 bits;
+//   a lo part below 2^-14 is off by at most 2^-25 absolute); two MFMAs per
+//   tile on the same code operand.
+//  bf16 pair: w * 2^-20 as a bf16 hi + lo pair (about 16 bits) against the
+//   codes as the bf16 128 + c, so the zero-point term carries -128 s; two
+//   MFMAs per tile.  Only for a chunk whose V scales leave [2^-10, 15.5] (then
+//   fp16 weights could overflow, p <= 2^8, or lose their normal range); its
+//   error is up to 2^-18 * 143 * s per unit of weight.
+// Every chunk whose scales allow takes the fp16 form if the error bound
+// below allows, else the fp16 pair; AMF_DECODE_MFMA_PRECISE takes the pair
+// throughout.
+//
+// Error bound of the fp16 form.  Rounding w to fp16 is off by at most
+// 2^-11 (w + 2^-14) (relative 2^-11 for a normal result, 2^-25 absolute for
+// a subnormal one), so the fp16 weights move output element d of row (r, g)
+// by at most 2^-11 * 15 * W / l, with codes c <= 15, W the sum of w + 2^-14
+// over the row-group's fp16 weights and l the row's softmax sum (every
+// chunk's tokens).  A chunk takes the fp16 form only if W <= kPv16Beta * l
+// holds afterwards for every row-group of the GQA group; then that error is
+// at most 2^-11 * 15 * kPv16Beta = 0.0147 for the finished row (both sides
+// scale alike under the online rescale, l only grows and W only by accepted
+// chunks) and for an LSE merge of such rows.  The check: lane (lo, hi) keeps
+// its k-slice's share of W; a chunk passes at once if every lane's share
+// stays <= kPv16Beta / 4 * lb, lb a lower bound of l (l when last taken,
+// rescaled alike), as the four shares then add up to at most kPv16Beta * l;
+// otherwise the shares are added across the k-slices and compared with the
+// current l (a row sum of l_run).  The weights' fp16 values stand in for w in
+// W (off by 2^-11 relative, inside the bound's rounding of 0.0147 to 0.015).
+#ifndef AMF_DECODE_PV16_BETA
+#define AMF_DECODE_PV16_BETA 2.0f
+#endif
+constexpr float kPv16Beta = AMF_DECODE_PV16_BETA;
+
+// Whether a chunk's V scales allow fp16 weights (0 or in [2^-10, 15.5]: no
+// weight overflows fp16 with p <= 2^8, and every token with p >= 2^-4 has a
+// normal weight): each lane checks the scale words of its 8 tokens, then the
+// wave votes.
+__device__ __forceinline__ bool pv_f16_range_ok(const u32x4& vp0, const u32x4& vp1) {
   uint32_t smax = 0;
 #pragma unroll
   for (int e = 0; e < 4; ++e) smax = max(smax, max(vp0[e] & 0xFFFFu, vp1[e] & 0xFFFFu));
   return !__any(smax > kF16ScaleMaxBits || (smax != 0u && smax < kF16ScaleMinBits));
 }
 
-// PV of one chunk from its V operands (read_chunk_v) and the weights in p_lds.
-template <int R, bool F16>
-__device__ __forceinline__ void chunk_pv(const u32x4& vc0, const u32x4& vc1, const u32x4& vp0,
-                                         const u32x4& vp1, int lo, int hi,
-                                         float (&corr)[(R + 3) / 4], f32x4 (&acc)[(R + 3) / 4][8],
-                                         float (&p_lds)[(R + 3) / 4][2][4][16]) {
+// The chunk's fp16 PV operand in the A layout: lane (lo, hi) holds row-group
+// (head 4T + lo/4, group lo%4) for tokens 8 hi .. 8 hi + 7 of the chunk, in
+// the operand order [t0 t4 t1 t5 t2 t6 t3 t7], 16 w for even and w for odd
+// tokens (also as fp16 pairs in h16, the operand's dwords); the zero-point
+// sum p * z goes to corr.  A token outside the
+// context or on a page with a bad id has p = +0 exactly (its score is -inf);
+// its param words may hold any bytes, and the legacy multiply (+0 * x = +0
+// for every x, NaN and infinities included) keeps them out.
+template <int R>
+__device__ __forceinline__ void pv_weights_f16(const u32x4& vp0, const u32x4& vp1, int lo, int hi,
+                                               float (&p_lds)[(R + 3) / 4][2][4][16],
+                                               u32x4 (&a16)[(R + 3) / 4],
+                                               f16x2_t (&h16)[(R + 3) / 4][4],
+                                               float (&corr)[(R + 3) / 4]) {
   constexpr int NT = (R + 3) / 4;
   const int vu = hi >> 1, vhalf = hi & 1;
   const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
-  const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
-  // Both paths accumulate O * 2^-24 (restored by the partial write).
-  //  fp16: weights w = p * s as one fp16 each (about 11 bits), codes as exact
-  //   fp16 subnormals; one MFMA per tile.  Used for a chunk whose V scales all
-  //   lie in [2^-10, 255] or are 0 (pv_f16_ok), so no weight overflows
-  //   (p <= 2^8) and the chunk's largest weights stay normal fp16 numbers.
-  //  bf16: weights w * 2^-24 as a bf16 hi + lo pair (about 16 bits), codes as
-  //   the bf16 128 + c, so the zero-point term carries -128 s.
-  if constexpr (F16) {
-    u32x4 a16[NT];
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
+    const float4 pa = pl[0], pb = pl[1];
+    const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+    float w[8];
+    float cs = corr[T];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float sv = pscale(pw[e]);
+      w[e] = mul_legacy(pv[e], (e & 1) ? sv : sv * 16.0f);
+      cs += mul_legacy(pv[e], pzero(pw[e]));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h16[T][j] = __builtin_convertvector((f32x2_t){w[j], w[j + 4]}, f16x2_t);
+      a16[T][j] = __builtin_bit_cast(uint32_t, h16[T][j]);
+    }
+    corr[T] = cs;
+  }
+}
+
+// The error bound above for the chunk's fp16 weights; on yes, they join
+// wsum (the lane's share of W).  lb holds the lower bound of l per lane (A
+// layout, head 4T + lo/4).
+template <int R>
+__device__ __forceinline__ bool pv_single_ok(int lo, const f16x2_t (&h16)[(R + 3) / 4][4],
+                                             const float (&l_run)[(R + 3) / 4],
+                                             float (&wsum)[(R + 3) / 4],
+                                             float (&lb)[(R + 3) / 4]) {
+  constexpr int NT = (R + 3) / 4;
+  const f16x2_t k_even = {(_Float16)0.0625f, (_Float16)0.0625f}, k_odd = {(_Float16)1.0f,
+                                                                          (_Float16)1.0f};
+  float cand[NT];
+  bool ok = true;
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    // the lane's 8 weights (pairs 0, 2 hold 16 w of even tokens) + 8 * 2^-14
+    float d = __builtin_amdgcn_fdot2(h16[T][1], k_odd, wsum[T] + 0x1p-11f, false);
+    d = __builtin_amdgcn_fdot2(h16[T][3], k_odd, d, false);
+    d = __builtin_amdgcn_fdot2(h16[T][0], k_even, d, false);
+    cand[T] = __builtin_amdgcn_fdot2(h16[T][2], k_even, d, false);
+    // rows past the GQA group carry scores of a zero query: never checked
+    const bool row_used = 4 * T + (lo >> 2) < R;
+    ok = ok && (!row_used || cand[T] <= (0.25f * kPv16Beta) * lb[T]);
+  }
+  if (__any(!ok)) {
+    ok = true;
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
-      // A row (r', g) = (4T + lo/4, lo%4), k-slice hi: tokens 8 hi .. 8 hi + 7.
-      const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
-      const float4 pa = pl[0], pb = pl[1];
-      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-      // A token outside the context or on a page with a bad id has p = +0
-      // exactly (its score is -inf); its param words may hold any bytes, and
-      // the legacy multiply (+0 * x = +0 for every x, NaN and infinities
-      // included) keeps them out of w and of the zero-point term.
-      float w[8];
-      float cs = corr[T];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float sv = pscale(pw[e]);
-        w[e] = mul_legacy(pv[e], (e & 1) ? sv * 0.0625f : sv);
-        cs += mul_legacy(pv[e], pzero(pw[e]));
-      }
-      a16[T] = u32x4{pk_f16(w[0], w[4]), pk_f16(w[1], w[5]), pk_f16(w[2], w[6]),
-                     pk_f16(w[3], w[7])};
-      corr[T] = cs;
+      float wrow = cand[T] + __shfl_xor(cand[T], 16);
+      wrow += __shfl_xor(wrow, 32);
+      // l of head 4T + lo/4: a row sum of the C layout (head 4T + hi), fetched
+      lb[T] = __shfl(row_sum16(l_run[T]), 16 * (lo >> 2));
+      const bool row_used = 4 * T + (lo >> 2) < R;
+      ok = ok && (!row_used || wrow <= kPv16Beta * lb[T]);
     }
-    // Dim block outermost: one block's code operand is live at a time.
+    if (__any(!ok)) return false;
+  }
+#pragma unroll
+  for (int T = 0; T < NT; ++T) wsum[T] = cand[T];
+  return true;
+}
+
+// PV of one chunk with single fp16 weights.
+template <int R>
+__device__ __forceinline__ void chunk_pv_f16(const uint8_t* slot, int lane,
+                                             const u32x4 (&a16)[(R + 3) / 4],
+                                             f32x4 (&acc)[(R + 3) / 4][8]) {
+  constexpr int NT = (R + 3) / 4;
+  u32x4 vc0, vc1;
+  read_chunk_vc(slot, lane, &vc0, &vc1);
+  const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
+  // Dim block outermost: one block's code operand is live at a time.
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const u32x4 vb = nib8_to_f16_sub(vw[b]);
+#pragma unroll
+    for (int T = 0; T < NT; ++T) acc[T][b] = mfma_f16(a16[T], vb, acc[T][b]);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// PV of one chunk with fp16 pairs, from the weights in p_lds and the slot's V
+// operands (the zero-point sum has been added).  One 16-row tile at a time,
+// so that one tile's pair is live (the code operand is rebuilt per tile).
+template <int R>
+__device__ __forceinline__ void chunk_pv_f16_pair(const uint8_t* slot, int lo, int hi,
+                                                  float (&p_lds)[(R + 3) / 4][2][4][16],
+                                                  f32x4 (&acc)[(R + 3) / 4][8]) {
+  constexpr int NT = (R + 3) / 4;
+  const int lane = lo + 16 * hi;
+  u32x4 vc0, vc1, vp0, vp1;
+  read_chunk_vc(slot, lane, &vc0, &vc1);
+  read_chunk_vp(slot, lane, &vp0, &vp1);
+  const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
+  const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
+  const int vu = hi >> 1, vhalf = hi & 1;
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
+    const float4 pa = pl[0], pb = pl[1];
+    const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+    u32x4 ah, al;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // operand pair (t_j, t_{j+4}): 16 w for even tokens, w for odd ones
+      const float sa = pscale(pw[j]), sb = pscale(pw[j + 4]);
+      const float wa = mul_legacy(pv[j], (j & 1) ? sa : sa * 16.0f);
+      const float wb = mul_legacy(pv[j + 4], (j & 1) ? sb : sb * 16.0f);
+      const uint32_t h = pk_f16(wa, wb);
+      ah[j] = h;
+      al[j] = pk_f16(wa - half_lo<false>(h), wb - half_hi<false>(h));
+    }
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       const u32x4 vb = nib8_to_f16_sub(vw[b]);
-#pragma unroll
-      for (int T = 0; T < NT; ++T) acc[T][b] = mfma_f16(a16[T], vb, acc[T][b]);
+      acc[T][b] = mfma_f16(ah, vb, acc[T][b]);
+      acc[T][b] = mfma_f16(al, vb, acc[T][b]);
     }
-  } else {
-    u32x4 ahi[NT], alo[NT];
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// PV of one chunk with bf16 hi + lo weights; the zero-point term carries the
+// codes' bias, -128 s per token, besides the zero point p * z.
+template <int R>
+__device__ __forceinline__ void chunk_pv_bf16(const uint8_t* slot, int lo, int hi,
+                                              float (&corr)[(R + 3) / 4],
+                                              f32x4 (&acc)[(R + 3) / 4][8],
+                                              float (&p_lds)[(R + 3) / 4][2][4][16]) {
+  constexpr int NT = (R + 3) / 4;
+  const int vu = hi >> 1, vhalf = hi & 1;
+  u32x4 vc0, vc1, vp0, vp1;
+  read_chunk_vc(slot, lo + 16 * hi, &vc0, &vc1);
+  read_chunk_vp(slot, lo + 16 * hi, &vp0, &vp1);
+  const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
+  const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
+  u32x4 ahi[NT], alo[NT];
 #pragma unroll
-    for (int T = 0; T < NT; ++T) {
-      const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
-      const float4 pa = pl[0], pb = pl[1];
-      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-      float wk[8];
-      float cs = corr[T];
+  for (int T = 0; T < NT; ++T) {
+    const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
+    const float4 pa = pl[0], pb = pl[1];
+    const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+    float wk[8];
+    float cs = corr[T];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float sv = pscale(pw[e]);
-        wk[k_of_nib(e)] = mul_legacy(pv[e], sv * kPvScale);
-        cs += mul_legacy(pv[e], pzero(pw[e]) - kCodeBias * sv);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t h, l;
-        pk_bf16_hilo(wk[2 * j], wk[2 * j + 1], &h, &l);
-        ahi[T][j] = h;
-        alo[T][j] = l;
-      }
-      corr[T] = cs;
+    for (int e = 0; e < 8; ++e) {
+      const float sv = pscale(pw[e]);
+      wk[k_of_nib(e)] = mul_legacy(pv[e], sv * kPvScale);
+      cs += mul_legacy(pv[e], pzero(pw[e]) - kCodeBias * sv);
     }
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const u32x4 vb = nib8_to_bf16_128c(vw[b]);
-#pragma unroll
-      for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(ahi[T], vb, acc[T][b]);
-#pragma unroll
-      for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(alo[T], vb, acc[T][b]);
+    for (int j = 0; j < 4; ++j) {
+      uint32_t h, l;
+      pk_bf16_hilo(wk[2 * j], wk[2 * j + 1], &h, &l);
+      ahi[T][j] = h;
+      alo[T][j] = l;
     }
+    corr[T] = cs;
+  }
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const u32x4 vb = nib8_to_bf16_128c(vw[b]);
+#pragma unroll
+    for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(ahi[T], vb, acc[T][b]);
+#pragma unroll
+    for (int T = 0; T < NT; ++T) acc[T][b] = mfma_bf16(alo[T], vb, acc[T][b]);
   }
   __builtin_amdgcn_wave_barrier();
 }
@@ -687,6 +851,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
   const int H = a.num_kv_heads;
   __shared__ __attribute__((aligned(16))) float p_lds[NT][2][4][16];
   __shared__ __attribute__((aligned(16))) uint8_t ring[D][kSlotBytes];
+  __shared__ __attribute__((aligned(16))) float qs_lds[NT][4][4];  // query group sums
 
   // ---- this wave's share: units (sequence, KV head, 32-token chunk) in that
   // order, units [w C / G, (w + 1) C / G) for wave w of G ----
@@ -754,7 +919,6 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     const float qk_scale = a.qk_scale_log2 * __builtin_ldexpf(1.0f, 24 + qe);
     const float qsum_down = __builtin_ldexpf(1.0f, -24 - qe);
     u32x4 qa[NT][4];
-    float qsum[NT][4];
   #pragma unroll
     for (int T = 0; T < NT; ++T) {
       const int r = 4 * T + (lo >> 2), g = lo & 3;
@@ -781,8 +945,8 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
         qa[T][st] = v;
       }
       // Qsum[r][g] = sum of q[r][32 g .. 32 g + 31]: lanes (lo, hi) add 8 of
-      // them, a cross-row sum completes it, then lane (t, j) fetches the four
-      // groups of head 4T + j.
+      // them, a cross-row sum completes it, and row hi = 0 stores it for the
+      // QK^T step, where lane (t, j) reads the four groups of head 4T + j.
       float part = 0.0f;
   #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -791,18 +955,20 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
       part = r < R ? part : 0.0f;
       part += __shfl_xor(part, 16);
       part += __shfl_xor(part, 32);
-  #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) qsum[T][gi] = __shfl(part, 4 * hi + gi) * qsum_down;
+      if (hi == 0) qs_lds[T][lo >> 2][lo & 3] = part * qsum_down;
     }
+    __builtin_amdgcn_wave_barrier();
 
 
-    float m_run[NT], l_run[NT], corr[NT];
+    float m_run[NT], l_run[NT], corr[NT], wsum[NT], lb[NT];
     f32x4 acc[NT][8];
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
       m_run[T] = kNegBig;
       l_run[T] = 0.0f;
       corr[T] = 0.0f;
+      wsum[T] = 0.0f;
+      lb[T] = 0.0f;
 #pragma unroll
       for (int b = 0; b < 8; ++b) acc[T][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -826,29 +992,36 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     #pragma unroll
       for (int k = 0; k + 1 < D; ++k)
         if (k < nch) issue(k);
-      // Chunks take the fp16 PV path until one whose V scales it cannot take;
-      // from that chunk on the split finishes on the bf16 path (a second loop, so
-      // that each loop keeps its own register footprint).
       auto qk = [&](int c) {
         dma_wait<D>(min(D - 1, nch - 1 - c));
         bool pok[2];
         split_page(spg, pi0 + 2 * c, &pok[0]);
         split_page(spg, pi0 + 2 * c + 1, &pok[1]);
-        chunk_qk<R>(ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa, qk_scale, qsum, m_run,
-                    l_run, corr, acc, p_lds);
+        chunk_qk<R>(ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa, qk_scale, qs_lds,
+                    m_run, l_run, corr, wsum, lb, acc, p_lds);
       };
+      // Chunks take fp16 weights, single where the error bound allows
+      // (pv_single_ok) and paired elsewhere, until one whose V scales fp16
+      // cannot take; from that chunk on the piece finishes on bf16 pairs (a
+      // second loop, so that each loop keeps its own register footprint).
       int c = 0;
       bool pending = false;  // chunk c has had QK^T and the softmax, not PV
       for (; c < nch; ++c) {
         if (c + D - 1 < nch) issue(c + D - 1);
         qk(c);
-        u32x4 vc0, vc1, vp0, vp1;
-        read_chunk_v(ring[c % D], lane, &vc0, &vc1, &vp0, &vp1);
-        if (!a.pv16 || !pv_f16_ok(vp0, vp1)) {
+        u32x4 vp0, vp1;
+        read_chunk_vp(ring[c % D], lane, &vp0, &vp1);
+        if (!pv_f16_range_ok(vp0, vp1)) {
           pending = true;
           break;
         }
-        chunk_pv<R, true>(vc0, vc1, vp0, vp1, lo, hi, corr, acc, p_lds);
+        u32x4 a16[NT];
+        f16x2_t h16[NT][4];
+        pv_weights_f16<R>(vp0, vp1, lo, hi, p_lds, a16, h16, corr);
+        if (a.pv16 && pv_single_ok<R>(lo, h16, l_run, wsum, lb))
+          chunk_pv_f16<R>(ring[c % D], lane, a16, acc);
+        else
+          chunk_pv_f16_pair<R>(ring[c % D], lo, hi, p_lds, acc);
       }
       for (; c < nch; ++c) {
         if (!pending) {
@@ -856,11 +1029,8 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
           qk(c);
         }
         pending = false;
-        u32x4 vc0, vc1, vp0, vp1;
-        read_chunk_v(ring[c % D], lane, &vc0, &vc1, &vp0, &vp1);
-        chunk_pv<R, false>(vc0, vc1, vp0, vp1, lo, hi, corr, acc, p_lds);
+        chunk_pv_bf16<R>(ring[c % D], lo, hi, corr, acc, p_lds);
       }
-
     }
 
     // ---- the segment's result: the output itself when the wave holds the

@@ -528,9 +528,11 @@ class DecodeCase:
         off = lay.code_offset(plane) if kind == "codes" else lay.param_offset(plane)
         return self.blob.data_ptr() + off
 
-    def launch(self, algo):
+    def launch(self, algo, out=None):
+        """One layer call into self.out (bf16), or into `out` (bf16 or fp32)."""
         h = self.amf_hip
-        rc = self._fn(self.q.data_ptr(), h.DTYPE_BF16, self.out.data_ptr(), h.DTYPE_BF16,
+        out = self.out if out is None else out
+        rc = self._fn(self.q.data_ptr(), h.DTYPE_BF16, out.data_ptr(), h.dtype_tag(out.dtype),
                       self.ptr(0, "codes"), self.ptr(0, "params"), self.ptr(1, "codes"),
                       self.ptr(1, "params"), self.pool, self.bt.data_ptr(), self.bt.shape[1],
                       self.dctx.data_ptr(), self.batch, self.q_heads, self.kv_heads, self.D, 16,

@@ -31,6 +31,10 @@ def attn_errors(got: np.ndarray, ref: np.ndarray) -> Tuple[float, float]:
 
 
 def check_attention(got: np.ndarray, ref: np.ndarray, max_abs: float = 2e-2,
-                    mean_rel: float = 1e-2) -> None:
+                    mean_rel: float = 1e-2, label: str = "") -> Tuple[float, float]:
+    """Asserts max-abs / mean-rel bounds and prints the measured errors."""
     ma, mr = attn_errors(got, ref)
+    print(f"attention error{' ' + label if label else ''}: max_abs={ma:.3e} mean_rel={mr:.3e} "
+          f"(bounds {max_abs:.0e} / {mean_rel:.0e})", flush=True)
     assert ma <= max_abs and mr <= mean_rel, f"max_abs={ma:.3e} mean_rel={mr:.3e}"
+    return ma, mr

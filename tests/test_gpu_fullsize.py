@@ -32,7 +32,7 @@ import bench
 from oracle import attention as oatt
 from oracle import codecs as oc
 
-from helpers import attn_errors
+from helpers import attn_errors, check_attention
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
@@ -163,6 +163,13 @@ def test_decode_fullsize_every_sequence():
         dc.launch(algo)
         torch.cuda.synchronize()
         outs[name] = dc.out.float().cpu().numpy()
+    # the default kernel with fp32 output: held to 2e-2 / 1e-2 without the
+    # bf16 output's own rounding
+    o32 = torch.empty(dc.out.shape, dtype=torch.float32, device=DEV)
+    dc.launch(amf_hip.DECODE_MFMA, out=o32)
+    torch.cuda.synchronize()
+    out32 = o32.cpu().numpy()
+    refs = []
     R = dc.q_heads // dc.kv_heads
     acc = {k: [0.0, 0.0, 0.0] for k in ("hip_vs_fallback", "fallback_vs_f64", "hip_vs_f64")}
 
@@ -180,6 +187,7 @@ def test_decode_fullsize_every_sequence():
                                     dc.ctx[b:b + 1].numpy())
         for name, out in outs.items():
             _check_f64(out[b:b + 1], ref, (name, b))
+        refs.append(ref[0])
         # the reference's own path: bf16 decompress, matmul -> softmax -> matmul in bf16
         kvb = kv32.to(torch.bfloat16)
         k = kvb[0].reshape(n * 16, dc.kv_heads, dc.D)[:ctx].permute(1, 0, 2)
@@ -191,6 +199,7 @@ def test_decode_fullsize_every_sequence():
         add("hip_vs_fallback", outs["mfma"][b], fb)
         add("fallback_vs_f64", fb, ref[0])
         add("hip_vs_f64", outs["mfma"][b], ref[0])
+    check_attention(out32, np.stack(refs), label="mfma fp32 output, 32 sequences")
     res = {k: (a[0], a[1] / a[2]) for k, a in acc.items()}
     for k, (ma, mr) in res.items():
         print(f"decode over 32 sequences, {k}: max-abs {ma:.3e}, mean-rel {mr:.3e}", flush=True)
@@ -239,12 +248,19 @@ def test_decode_70b_every_sequence():
         pytest.skip("needs device memory")
     dc = bench.DecodeCase(8, 64, 8, 131072, 131072, 6)
     dc.launch(amf_hip.DECODE_MFMA)
+    o32 = torch.empty(dc.out.shape, dtype=torch.float32, device=DEV)
+    dc.launch(amf_hip.DECODE_MFMA, out=o32)
     torch.cuda.synchronize()
     out = dc.out.float().cpu().numpy()
+    out32 = o32.cpu().numpy()
+    refs = []
     for b in range(dc.batch):
         ctx, n, kv32 = _seq_kv(dc, b)
         ref = oatt.paged_decode_f64(dc.q[b:b + 1].float().cpu().numpy(), kv32[0].numpy(),
                                     kv32[1].numpy(), np.arange(n)[None], dc.ctx[b:b + 1].numpy())
         _check_f64(out[b:b + 1], ref, ("mfma70b", b))
+        refs.append(ref[0])
+    # fp32 output: 2e-2 / 1e-2 without the bf16 output's own rounding
+    check_attention(out32, np.stack(refs), label="mfma fp32 output, 70B shape")
     del dc
     torch.cuda.empty_cache()

@@ -548,18 +548,17 @@ def test_int4_paged_decode_shares_span_many_pairs():
     q, bt, ctx, pool, codes, params, kv32 = _decode_case(R, Hkv, ctxs, seed=92)
     ref = oatt.paged_decode_f64(q.float().numpy(), kv32[0].numpy(), kv32[1].numpy(), bt.numpy(),
                                 ctx.numpy())
-    # bf16 hi/lo PV weights: the work map's indexing checked to a tight bound
-    got, flag = _run_decode(q, bt, ctx, pool, codes, params, Hkv, amf_hip.DECODE_MFMA_PRECISE)
-    assert flag == 0
-    check_attention(got, ref, max_abs=5e-3, mean_rel=2e-4)
-    assert np.all(got[np.asarray(ctxs) == 0] == 0.0)
-    # fp16 PV weights (about 11 bits each): short contexts leave a few tokens
-    # with most of the weight, against V rows with x20 outlier channels, so
-    # 2.2 M outputs reach a larger worst case than the longer tests
-    got, flag = _run_decode(q, bt, ctx, pool, codes, params, Hkv, amf_hip.DECODE_MFMA)
-    assert flag == 0
-    check_attention(got, ref, max_abs=4e-2, mean_rel=1e-3)
-    assert np.all(got[np.asarray(ctxs) == 0] == 0.0)
+    # every algorithm within the stated tolerance on fp32 output; the default
+    # MFMA kernel keeps these short, peaked rows on precise PV weights (its
+    # fp16 weights only where their rounding error budget allows)
+    for algo in DECODE_ALGOS:
+        got, flag = _run_decode(q, bt, ctx, pool, codes, params, Hkv, algo)
+        assert flag == 0
+        check_attention(got, ref, label=f"algo {algo}")
+        assert np.all(got[np.asarray(ctxs) == 0] == 0.0)
+        if algo == amf_hip.DECODE_MFMA_PRECISE:
+            # bf16 hi/lo PV weights throughout: the work map's indexing to a tight bound
+            check_attention(got, ref, max_abs=5e-3, mean_rel=2e-4, label="precise, tight")
 
 
 @pytest.mark.parametrize("algo", DECODE_ALGOS)
