@@ -97,6 +97,7 @@ struct DecodeArgs {
   int num_seqs;
   int stream_k;          // MFMA path: waves take equal shares of the (sequence, KV head, chunk) space
   int sk_waves;          // grid size of the stream-K decode launch
+  int64_t* sk_meta;      // stream-K: units before each sequence [num_seqs], then all units
 };
 
 // ---- lane helpers -----------------------------------------------------------
@@ -860,6 +861,9 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
   // spanning a pair all hold a part of it (the rest exit).
   const int64_t G = min((int64_t)a.sk_waves, total), w = blockIdx.x;
   if (w >= G) return;
+  // The merge finds a pair's waves from the units before its sequence, which
+  // the wave holding the sequence's first unit records, and from the total.
+  if (w == 0 && lane == 0) a.sk_meta[a.num_seqs] = total;
   const int64_t u0 = uni64(w * total / G), u1 = uni64((w + 1) * total / G);
   if (u0 >= u1) return;
   int s = 0;
@@ -874,6 +878,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
       ++s;
       continue;
     }
+    if (u == P && lane == 0) a.sk_meta[s] = P;
     const int h = uni32((int)((u - P) / nch_s));
     const int64_t pair0 = uni64(P + (int64_t)h * nch_s), pair1 = pair0 + nch_s;
     const int64_t seg_end = uni64(min(u1, pair1));
@@ -1233,7 +1238,125 @@ __global__ __launch_bounds__(64) void int4_decode_valu_kernel(DecodeArgs a) {
 
 // ================================================================ merge ====
 
-// One workgroup of four waves per (query head, sequence):
+// Stream-K merge: one wave per (query head, sequence).  The pair's parts are
+// the slots of waves wf..wl (the first one's slot 1 when its share began in
+// an earlier pair), found from the units before the sequence (sk_meta, written
+// by the decode launch) with the decode's own share arithmetic; a pair one
+// wave held was finished by it.  Lane k reads (m, l) of part k; lane (half, c)
+// reads dims 4c .. 4c + 3 of parts half, half + 2, ...; the first kSkPre of
+// those are loaded with the (m, l) words, before the maximum is known, so the
+// merge waits on memory once for up to 2 kSkPre parts.  A map entry that
+// this call's decode launch did not write raises AMF_ERRFLAG_SYNC (the
+// output is then invalid) and is never used as an address.
+constexpr int kSkPre = 8;
+
+template <int OUT_DTYPE>
+__global__ __launch_bounds__(64) void int4_decode_merge_sk_kernel(DecodeArgs a) {
+  const int qhd = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
+  const int half = lane >> 5, c = lane & 31;
+  const int R = a.num_q_heads / a.num_kv_heads;
+  // context length and the map are independent loads; an empty sequence
+  // (no units) never reads its map entry's value
+  const int64_t nch = sk_chunks(a, s);
+  const int64_t P = a.sk_meta[s], total = a.sk_meta[a.num_seqs];
+  float L = 0.0f;
+  float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t H = a.num_kv_heads;
+  // a map entry outside [0, total - H nch] (not written by this call's decode
+  // launch) is reported and leaves zeros instead of reading outside the slots
+  const bool map_ok = P >= 0 && total > 0 && P <= total - H * nch;
+  if (nch > 0 && !map_ok && lane == 0 && a.err_flag) atomicOr(a.err_flag, AMF_ERRFLAG_SYNC);
+  if (nch > 0 && map_ok) {
+    const int64_t G = min((int64_t)a.sk_waves, total);  // as the decode launch uses it
+    const int64_t pair0 = P + (int64_t)(qhd / R) * nch;
+    const int64_t wf = sk_wave_of(pair0, total, G);
+    const int64_t wl = sk_wave_of(pair0 + nch - 1, total, G);
+    if (wf == wl) return;  // one wave held the whole pair and wrote the output
+    const int n_sp = (int)(wl - wf + 1);
+    const bool first_slot1 = wf * total / G < pair0;
+    const float* base = a.ws + (wf * 2 * R + qhd % R) * kPartStride;
+    auto part = [&](int k) -> const float* {
+      const int slot = (k == 0 && first_slot1) ? 1 : 0;
+      return base + (int64_t)((2 * k + slot) * R) * kPartStride;
+    };
+    // accumulators of parts half, half + 2, ... (rows clamped into the pair's
+    // parts; a clamped row is loaded but never added)
+    float4 pre[kSkPre];
+#pragma unroll
+    for (int j = 0; j < kSkPre; ++j)
+      pre[j] = *reinterpret_cast<const float4*>(part(min(half + 2 * j, n_sp - 1)) + 4 * c);
+    float m0 = kNegBig, l0 = 0.0f;
+    if (lane < n_sp) {
+      const float2 ml = *reinterpret_cast<const float2*>(part(lane) + kD);
+      m0 = ml.x;
+      l0 = ml.y;
+    }
+    float M = m0;
+    for (int k = lane + 64; k < n_sp; k += 64) M = fmaxf(M, part(k)[kD]);
+    M = wave_max_xor(M, 64);
+    for (int k0 = 0; k0 < n_sp; k0 += 64) {
+      float wk = 0.0f;
+      if (k0 + lane < n_sp) {
+        float mk = m0, lk = l0;
+        if (k0 != 0) {
+          const float2 ml = *reinterpret_cast<const float2*>(part(k0 + lane) + kD);
+          mk = ml.x;
+          lk = ml.y;
+        }
+        wk = exp2_fast(mk - M);
+        L += wk * lk;
+      }
+      const int cnt = min(64, n_sp - k0);
+      int j0 = 0;
+      if (k0 == 0) {
+#pragma unroll
+        for (int j = 0; j < kSkPre; ++j) {
+          const float wj = __shfl(wk, half + 2 * j);  // every lane shuffles
+          if (half + 2 * j < cnt) {
+            o.x += wj * pre[j].x;
+            o.y += wj * pre[j].y;
+            o.z += wj * pre[j].z;
+            o.w += wj * pre[j].w;
+          }
+        }
+        j0 = 2 * kSkPre;
+      }
+#pragma unroll 4
+      for (int j = j0; j < cnt; j += 2) {
+        const int jj = j + half;
+        const float wj = __shfl(wk, min(jj, 63));
+        if (jj < cnt) {
+          const float4 v = *reinterpret_cast<const float4*>(part(k0 + jj) + 4 * c);
+          o.x += wj * v.x;
+          o.y += wj * v.y;
+          o.z += wj * v.z;
+          o.w += wj * v.w;
+        }
+      }
+    }
+    o.x += __shfl_xor(o.x, 32);
+    o.y += __shfl_xor(o.y, 32);
+    o.z += __shfl_xor(o.z, 32);
+    o.w += __shfl_xor(o.w, 32);
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+  }
+  if (half != 0) return;
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  const int64_t row = ((int64_t)s * a.num_q_heads + qhd) * kD;
+  if constexpr (OUT_DTYPE == AMF_DTYPE_F32) {
+    float* out = static_cast<float*>(a.out) + row;
+    *reinterpret_cast<float4*>(out + 4 * c) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+  } else {
+    constexpr bool BF = OUT_DTYPE == AMF_DTYPE_BF16;
+    uint16_t* out = static_cast<uint16_t*>(a.out) + row;
+    const uint32_t p0 = (uint32_t)oval<BF>(o.x * inv) | ((uint32_t)oval<BF>(o.y * inv) << 16);
+    const uint32_t p1 = (uint32_t)oval<BF>(o.z * inv) | ((uint32_t)oval<BF>(o.w * inv) << 16);
+    *reinterpret_cast<uint2*>(out + 4 * c) = uint2{p0, p1};
+  }
+}
+
+// Split merge (fixed splits of the VALU path): one workgroup of four waves
+// per (query head, sequence):
 // O = sum_i 2^(m_i - M) acc_i / L, written as OUT_DTYPE (an AMF_DTYPE_* tag).
 // Thread t reads (m, l) of split t once (and of splits t + 256, ... when
 // there are more) and the weights are shared through LDS.  For the
@@ -1253,53 +1376,9 @@ __global__ __launch_bounds__(kMergeThreads) void int4_decode_merge_kernel(Decode
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int half = lane >> 5, c = lane & 31;
   const int ctx = clamp_context(a, s);
-  int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
+  const int n_sp = (ctx + a.split_tokens - 1) / a.split_tokens;
   const float* base = a.ws + ((int64_t)s * a.num_q_heads + qhd) * a.max_splits * kPartStride;
-  // Stream-K decode: the parts of (s, KV head) are the slots of waves wf..wl
-  // (the first one's slot 1 when its share began in an earlier pair).
-  const int R = a.num_q_heads / a.num_kv_heads;
-  int64_t wf = 0;
-  bool first_slot1 = false;
-  if (a.stream_k) {
-    const int64_t nch = sk_chunks(a, s);
-    n_sp = 0;
-    if (nch > 0) {
-      int64_t t_all = 0, t_before = 0;
-      for (int i = tid; i < a.num_seqs; i += kMergeThreads) {
-        const int64_t c = sk_chunks(a, i);
-        t_all += c;
-        t_before += i < s ? c : 0;
-      }
-      t_all = wave_sum_i64(t_all);
-      t_before = wave_sum_i64(t_before);
-      __shared__ int64_t s_cnt[2][kMergeWaves];
-      if (lane == 0) {
-        s_cnt[0][w] = t_all;
-        s_cnt[1][w] = t_before;
-      }
-      __syncthreads();
-      t_all = 0;
-      t_before = 0;
-#pragma unroll
-      for (int i = 0; i < kMergeWaves; ++i) {
-        t_all += s_cnt[0][i];
-        t_before += s_cnt[1][i];
-      }
-      const int64_t H = a.num_kv_heads, total = t_all * H;
-      const int64_t G = min((int64_t)a.sk_waves, total);  // as the decode launch uses it
-      const int64_t pair0 = t_before * H + (int64_t)(qhd / R) * nch;
-      wf = sk_wave_of(pair0, total, G);
-      const int64_t wl = sk_wave_of(pair0 + nch - 1, total, G);
-      if (wf == wl) return;  // one wave held the whole pair and wrote the output
-      n_sp = (int)(wl - wf + 1);
-      first_slot1 = wf * total / G < pair0;
-    }
-  }
-  auto part = [&](int k) -> const float* {
-    if (!a.stream_k) return base + (int64_t)k * kPartStride;
-    const int64_t slot = (k == 0 && first_slot1) ? 1 : 0;
-    return a.ws + (((wf + k) * 2 + slot) * R + qhd % R) * kPartStride;
-  };
+  auto part = [&](int k) -> const float* { return base + (int64_t)k * kPartStride; };
   // The accumulators of this thread's first kMergePre splits are loaded
   // together with the (m, l) words, before the maximum is known, so the merge
   // waits on memory once (rows clamped into the sequence's splits; a clamped
@@ -1524,9 +1603,12 @@ extern "C" int64_t amf_int4_decode_workspace_bytes(int32_t num_seqs, int32_t num
                               kPartStride * (int64_t)sizeof(float);
   const int R = num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 ? num_q_heads / num_kv_heads
                                                                      : 1;
+  // stream-K: two partial slots per resident wave, then the map of sequence
+  // starts (num_seqs + 1 int64)
   const int64_t sk_bytes =
       (R == 1 || R == 2 || R == 4 || R == 8)
-          ? (int64_t)sk_waves(R) * 2 * R * kPartStride * (int64_t)sizeof(float)
+          ? (int64_t)sk_waves(R) * 2 * R * kPartStride * (int64_t)sizeof(float) +
+                ((int64_t)num_seqs + 1) * (int64_t)sizeof(int64_t)
           : 0;
   return std::max(split_bytes, sk_bytes);
 }
@@ -1608,6 +1690,10 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
   a.sk_waves = a.stream_k ? sk_waves(R) : 0;
   if (a.stream_k && a.sk_waves <= 0)
     return fail(AMF_ERR_RUNTIME, "%s: could not size the decode grid (device occupancy query)", who);
+  a.sk_meta = a.stream_k ? reinterpret_cast<int64_t*>(
+                               static_cast<uint8_t*>(workspace) +
+                               (int64_t)a.sk_waves * 2 * R * kPartStride * (int64_t)sizeof(float))
+                         : nullptr;
   // Stream-K unit arithmetic stays in int64: units x waves < 2^62.
   if (a.stream_k && ((int64_t)max_context_len / 32 + 1) * num_seqs * num_kv_heads >
                         ((int64_t)1 << 62) / a.sk_waves)
@@ -1640,12 +1726,20 @@ extern "C" int amf_int4_paged_decode_attn(const void* q, int32_t q_dtype, void* 
 #undef AMF_LAUNCH
   }
   dim3 mgrid((unsigned)num_q_heads, (unsigned)num_seqs);
-  if (out_dtype == AMF_DTYPE_BF16)
+  if (a.stream_k) {
+    if (out_dtype == AMF_DTYPE_BF16)
+      int4_decode_merge_sk_kernel<AMF_DTYPE_BF16><<<mgrid, 64, 0, st>>>(a);
+    else if (out_dtype == AMF_DTYPE_F16)
+      int4_decode_merge_sk_kernel<AMF_DTYPE_F16><<<mgrid, 64, 0, st>>>(a);
+    else
+      int4_decode_merge_sk_kernel<AMF_DTYPE_F32><<<mgrid, 64, 0, st>>>(a);
+  } else if (out_dtype == AMF_DTYPE_BF16) {
     int4_decode_merge_kernel<AMF_DTYPE_BF16><<<mgrid, kMergeThreads, 0, st>>>(a);
-  else if (out_dtype == AMF_DTYPE_F16)
+  } else if (out_dtype == AMF_DTYPE_F16) {
     int4_decode_merge_kernel<AMF_DTYPE_F16><<<mgrid, kMergeThreads, 0, st>>>(a);
-  else
+  } else {
     int4_decode_merge_kernel<AMF_DTYPE_F32><<<mgrid, kMergeThreads, 0, st>>>(a);
+  }
   return check_launch(who);
 }
 

@@ -258,14 +258,17 @@ int amf_int4_dequant_scatter(int32_t format,
  * max_context_len bounds every context_lens[i] (it sizes the grid: no
  * device-to-host sync); a sequence with context 0 gets zeros.
  * softmax_scale <= 0 selects 1/sqrt(head_dim).
- * workspace: split partials, amf_int4_decode_workspace_bytes() bytes (it
- *              sizes the MFMA path for the current device's resident waves:
- *              call it with the device of the launch current).
+ * workspace: split partials and, for the MFMA path, a map of the
+ *              sequences' first work units (num_seqs + 1 int64);
+ *              amf_int4_decode_workspace_bytes() bytes (it sizes the MFMA
+ *              path for the current device's resident waves: call it with
+ *              the device of the launch current).
  * algo: AMF_DECODE_AUTO (= AMF_DECODE_MFMA), AMF_DECODE_VALU,
- *       AMF_DECODE_MFMA (PV products on fp16 weights wherever a 32-token
- *       chunk's V scales are 0 or in [2^-10, 255], bf16 hi/lo pairs
- *       elsewhere) or AMF_DECODE_MFMA_PRECISE (bf16 hi/lo pairs throughout:
- *       about 10x less PV rounding error, 7-12% slower).
+ *       AMF_DECODE_MFMA (PV products on single fp16 weights for a 32-token
+ *       chunk only while their rounding error stays provably within 0.015
+ *       of the output, fp16 hi + lo pairs elsewhere, bf16 hi + lo pairs where
+ *       a chunk's V scales leave [2^-10, 15.5]) or AMF_DECODE_MFMA_PRECISE
+ *       (pairs throughout).
  * Supported: head_dim 128, block_size 16, num_q_heads / num_kv_heads in
  * {1, 2, 4, 8}; anything else returns AMF_ERR_UNSUPPORTED.
  * Replaces int4_decode_attention (int4_decode_attention.py:6-9 ->

@@ -82,10 +82,20 @@ def test_noalloc_matches_workspace_entry_point(R, out_dtype):
 def test_noalloc_refuses_more_than_its_scratch():
     lib = amf_hip.load()
     dev, host = _case(3, 2, 2, 4, 100, 20)
-    out = torch.full((2, 8, D), 3.0, dtype=torch.float32, device=DEV)
-    big = dict(host, S=1024, width=8192)   # 1024 seqs x 8 heads x 131072 tokens of partials
-    assert amf_hip.decode_workspace_bytes(1024, 8, 2, D, 8192 * 16) > 64 << 20
-    rc = _call(lib, dev, big, out, amf_hip.DTYPE_F32, None)
+    # 1024 sequences x 8 heads x 131072 tokens of partials.  Every buffer is
+    # allocated at that shape (the block table, 32 MiB of zeros, names page 0
+    # of the 20-page pool; contexts are 50 tokens), so that a broken size
+    # check would launch kernels that stay inside their buffers and the
+    # asserts below, not a memory fault, report it.
+    S, width = 1024, 8192
+    assert amf_hip.decode_workspace_bytes(S, 8, 2, D, width * 16) > 64 << 20
+    big_dev = dict(dev, q=torch.zeros(S, 8, D, dtype=torch.bfloat16, device=DEV),
+                   bt=torch.zeros(S, width, dtype=torch.int32, device=DEV),
+                   ctx=torch.full((S,), 50, dtype=torch.int32, device=DEV))
+    big = dict(host, S=S, width=width)
+    out = torch.full((S, 8, D), 3.0, dtype=torch.float32, device=DEV)
+    torch.cuda.synchronize()
+    rc = _call(lib, big_dev, big, out, amf_hip.DTYPE_F32, None)
     assert rc == amf_hip.ERR_WORKSPACE and b"scratch" in lib.amf_last_error()
     torch.cuda.synchronize()
     assert bool((out == 3.0).all())
