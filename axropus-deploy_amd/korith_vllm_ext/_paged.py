@@ -227,26 +227,32 @@ def _kv_planes(layer: torch.Tensor):
 
 # Geometry of recently seen cache lists, by the identity of their tensors
 # (weak references: a cached entry never keeps a cache alive, and a freed
-# tensor whose id is reused fails the identity check).  A view only reads
-# shapes, strides and addresses, which a live tensor object keeps (vLLM
-# allocates its KV caches once), so a hit skips the per-layer attribute reads.
+# tensor whose id is reused fails the identity check).  A hit also requires
+# every tensor's address, shape and strides to be the ones the view was built
+# from: a live tensor whose storage was swapped in place (set_, resize_,
+# .data =) misses and is measured again, so no launch gets stale addresses
+# or a stale page count.
 _VIEWS: "OrderedDict[tuple, tuple]" = OrderedDict()
 _VIEWS_MAX = 64
+
+
+def _layout_sig(t: torch.Tensor) -> tuple:
+    return (t.data_ptr(), t.shape, t.stride())
 
 
 def cache_view(gpu_cache: Sequence[torch.Tensor]) -> CacheView:
     key = tuple(map(id, gpu_cache))
     hit = _VIEWS.get(key)
     if hit is not None:
-        refs, v = hit
-        if all(r() is t for r, t in zip(refs, gpu_cache)):
+        refs, sigs, v = hit
+        if all(r() is t and _layout_sig(t) == sg for r, sg, t in zip(refs, sigs, gpu_cache)):
             _VIEWS.move_to_end(key)
             return CacheView(v.planes, v.page_stride, v.pool_pages, v.block_size, v.num_heads,
                              v.head_dim, v.dtype, v.device, keep=list(gpu_cache))
     view = _make_cache_view(gpu_cache)
     geom = CacheView(view.planes, view.page_stride, view.pool_pages, view.block_size,
                      view.num_heads, view.head_dim, view.dtype, view.device, keep=[])
-    _VIEWS[key] = ([weakref.ref(t) for t in gpu_cache], geom)
+    _VIEWS[key] = ([weakref.ref(t) for t in gpu_cache], [_layout_sig(t) for t in gpu_cache], geom)
     while len(_VIEWS) > _VIEWS_MAX:
         _VIEWS.popitem(last=False)
     return view

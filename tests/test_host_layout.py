@@ -81,6 +81,25 @@ def test_cache_view_shapes():
         _paged.cache_view([])
 
 
+def test_cache_view_memo_sees_storage_swapped_in_place():
+    """A memoized view is reused only while every tensor keeps the address,
+    shape and strides it was built from: set_ / resize_ / .data = on a live
+    tensor give a fresh view (addresses and page count)."""
+    layers = [torch.zeros(2, 10, 16, 2, 64, dtype=torch.bfloat16) for _ in range(2)]
+    v1 = _paged.cache_view(layers)
+    assert _paged.cache_view(layers).planes == v1.planes          # memo hit
+    layers[1].set_(torch.zeros(2, 10, 16, 2, 64, dtype=torch.bfloat16))
+    v2 = _paged.cache_view(layers)
+    assert v2.planes[:2] == v1.planes[:2] and v2.planes[2] == layers[1].data_ptr()
+    assert v2.planes[2] != v1.planes[2]
+    layers[0].data = torch.zeros(2, 6, 16, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):                               # 6 vs 10 pages now
+        _paged.cache_view(layers)
+    layers[1].data = torch.zeros(2, 6, 16, 2, 64, dtype=torch.bfloat16)
+    v3 = _paged.cache_view(layers)
+    assert v3.pool_pages == 6 and v3.planes[0] == layers[0].data_ptr()
+
+
 def test_dense_view_pads_tokens():
     x = torch.randn(3, 20, 2, 64).to(torch.bfloat16)
     v, n, xp = _paged.dense_view(x, 16)
