@@ -58,6 +58,18 @@ inline uint32_t coop_spin_limit() {
   return limit;
 }
 
+// AMF_NO_COOP set to a non-zero value in the environment (read once) turns
+// the cooperative launches off: per-tensor FP8 saves then take the two-pass
+// kernels.  For processes that cannot have a cooperative launch (a profiler
+// that does not survive one, a caller capturing into a graph).
+inline bool coop_disabled() {
+  static const bool off = [] {
+    const char* e = getenv("AMF_NO_COOP");
+    return e && strtol(e, nullptr, 10) != 0;
+  }();
+  return off;
+}
+
 __device__ __forceinline__ uint32_t* coop_line(uint32_t* sync, int gi, int k) {
   return sync + ((int64_t)gi * (kCoopClusters + 1) + k) * kLineWords;
 }

@@ -706,7 +706,7 @@ int try_tensor_coop(int32_t dt, const uint64_t* cache_planes, int64_t cache_page
                     const int32_t* block_ids, int64_t pool_pages, const uint64_t* code_planes,
                     int64_t n_pages, const PageGeom& g, int n_groups, uint32_t* ws,
                     int32_t* err_flag, hipStream_t s) {
-  if (!aligned16(cache_page_stride)) return kCoopNotTaken;
+  if (coop_disabled() || !aligned16(cache_page_stride)) return kCoopNotTaken;
   const int64_t page_elems = (int64_t)g.n_rows * g.head_dim;
   const int64_t chunks_pp = page_elems / 8;  // head_dim % 16 == 0: whole 16-byte chunks
   if (chunks_pp % kCoopThreads != 0) return kCoopNotTaken;

@@ -199,8 +199,11 @@ int amf_kv_scatter_slots(const uint64_t* in_planes, int64_t in_row_stride,
  * its contents on entry do not matter.  The per-tensor format reads the cache
  * once through a cooperative launch when the device supports it and a scale
  * group (planes_per_scale planes of n_pages pages, at least 4 MiB) fits the
- * resident grid, and twice (absmax kernel, then quantize kernel) otherwise;
- * both give the same bytes.  A cooperative wait that gives up (never in a
+ * resident grid, and twice (absmax kernel, then quantize kernel) otherwise
+ * or when AMF_NO_COOP is set to a non-zero value in the environment (read
+ * once; for processes that cannot have a cooperative launch, such as a
+ * profiler session or graph capture); both give the same bytes.  A
+ * cooperative wait that gives up (never in a
  * correct launch) raises AMF_ERRFLAG_SYNC and writes an infinite scale for
  * its group.
  * Replaces compressed_vram_pool.py:481-508 with FP8E4M3Codec.compress

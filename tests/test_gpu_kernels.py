@@ -201,6 +201,40 @@ def test_fp8_tensor_single_read_bitexact(dtype, geom):
         assert torch.equal(side, oc.fp8_sidecar(scale)), l
 
 
+def _tensor_save_digest(dtype, geom):
+    import hashlib
+    values, src_ids, _ = _codec_case(dtype, 12, geom)
+    L, n, bs, H, D = geom["L"], geom["n"], geom["bs"], geom["H"], geom["D"]
+    view = _paged.cache_view(_cache_from(values))
+    layout = _paged.BlobLayout("fp8_e4m3", 2, n, bs, H, D)
+    blobs = [torch.zeros(layout.total_bytes, dtype=torch.uint8, device=DEV) for _ in range(L)]
+    _paged.quant_gather(layout, view, src_ids, [b.data_ptr() for b in blobs], 2)
+    torch.cuda.synchronize()
+    return hashlib.sha256(b"".join(bytes_of(b).tobytes() for b in blobs)).hexdigest()
+
+
+def test_fp8_tensor_no_coop_environment_same_bytes():
+    """AMF_NO_COOP=1 (read once per process, so checked in a child process)
+    sends a per-tensor save that the single-read kernel would take to the
+    two-pass kernels: same bytes."""
+    import os
+    import subprocess
+    import sys
+    geom = dict(L=3, pool=512, n=160, bs=16, H=8, D=128)
+    want = _tensor_save_digest(torch.bfloat16, geom)
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    paths = [here, root, os.path.join(root, "axropus-deploy_amd")]
+    code = ("import sys, torch; sys.path[:0] = %r; import test_gpu_kernels as T; "
+            "print(T._tensor_save_digest(torch.bfloat16, %r))" % (paths, geom))
+    env = dict(os.environ, AMF_NO_COOP="1")
+    print("child process: per-tensor save with AMF_NO_COOP=1", flush=True)
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         timeout=240, cwd=root)
+    assert out.returncode == 0, out.stderr[-2000:]
+    assert out.stdout.strip().splitlines()[-1] == want
+
+
 def test_fp8_tensor_single_read_beside_another_stream():
     """The cooperative per-tensor save issued while restores run on a second
     stream (default priority): it completes without a sync give-up and its
