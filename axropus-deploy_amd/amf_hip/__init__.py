@@ -18,7 +18,7 @@ import threading
 from collections import OrderedDict
 from typing import Optional, Sequence
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # status codes
 OK = 0
@@ -125,7 +125,14 @@ SIGNATURES = {
     "amf_dense_attn": (
         _c_i32,
         [_c_ptr, _c_ptr, _c_ptr, _c_i32, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i32,
-         _c_i64, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_ptr],
+         _c_i64, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_ptr, _c_i64, _c_ptr],
+    ),
+    "amf_dense_attn_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i64, _c_i64, _c_i32]),
+    "amf_int4_sym_dense_attn": (
+        _c_i32,
+        [_c_ptr, _c_i32, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_ptr, _c_i32, _c_i64, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_ptr, _c_i64,
+         _c_ptr],
     ),
     "amf_direct_kv_init": (_c_ptr, [_c_u64]),
     "amf_direct_kv_free": (None, [_c_ptr]),

@@ -8,13 +8,28 @@
 // (num_q_heads a multiple of num_kv_heads); the reference's matmul broadcast
 // allows only equal head counts or a single KV head.
 //
-// One workgroup (4 waves) per query row.  Wave w takes the 64-token chunks
-// w, w+4, w+8, ...; lane l scores token chunk_base + l against the query held
-// in LDS, the wave keeps an online softmax (running max and sum), and the PV
+// Split path (head_dim 64, 128 or 256, a caller workspace): flash decoding.
+// The KV tokens of a row are cut into splits sized so that the launch has
+// about kSplitWaves waves; one wave per (query row, split) streams its tokens
+// in 64-token chunks.  A K or V row is D / 8 lanes wide (16-byte loads, 8
+// elements per lane), so one wave load covers 64 / (D / 8) whole rows; the
+// score of a token is a reduction over its row's lanes, the online softmax
+// runs per lane on its rows' scores, and the PV product accumulates 8 dims
+// per lane.  Each split leaves (max, sum, acc[D]) in the workspace and a
+// merge kernel combines a row's splits with an LSE rescale.  The query rows
+// of one KV head are neighbouring waves, so their shared K/V rows are read
+// from HBM about once.
+//
+// Single-pass path (other head dims, kv_len 0, or no workspace): one
+// workgroup (4 waves) per query row.  Wave w takes the 64-token chunks w,
+// w+4, w+8, ...; lane l scores token chunk_base + l against the query held in
+// LDS, the wave keeps an online softmax (running max and sum), and the PV
 // product is lane-parallel over head_dim with the chunk's probabilities
 // broadcast by readlane.  The four partial (max, sum, acc) triples are merged
 // through LDS.
 #include <math.h>
+
+#include <algorithm>
 
 #include "amf_internal.h"
 #include "amf_kernel_util.h"
@@ -42,6 +57,11 @@ struct AttnArgs {
   int64_t q_len, kv_len;
   int32_t head_dim;
   float scale;
+  // INT4_SYM K/V (split path only): k and v point at packed codes (element
+  // 8 w + n of a row in nibble n of code word w), these at the fp16
+  // per-channel scales [head_dim].
+  const _Float16* k_scales;
+  const _Float16* v_scales;
 };
 
 template <int DT>
@@ -195,6 +215,376 @@ __global__ __launch_bounds__(kThreads) void dense_attn_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------- split path --
+
+#ifndef AMF_DENSE_SPLIT_WAVES
+#define AMF_DENSE_SPLIT_WAVES 4096
+#endif
+constexpr int64_t kSplitWaves = AMF_DENSE_SPLIT_WAVES;  // waves one launch aims for
+constexpr int kPartPad = 4;            // a split partial: acc[D], m, l, 2 pad (16-byte rows)
+constexpr int64_t kXcds = 8;           // XCDs of the chip, dealt workgroups round-robin
+
+// Splits per row and tokens per split (a multiple of 64) for `rows` query
+// rows over kv_len tokens: about kSplitWaves waves in all, at most one split
+// per 64-token chunk.
+inline void dense_splits(int64_t rows, int64_t kv_len, int64_t* n_splits, int64_t* split_tokens) {
+  const int64_t chunks = (kv_len + 63) / 64;
+  int64_t n = (kSplitWaves + rows - 1) / rows;
+  n = std::max<int64_t>(1, std::min<int64_t>(n, chunks));
+  const int64_t per = (chunks + n - 1) / n;  // chunks per split
+  *split_tokens = per * 64;
+  *n_splits = (chunks + per - 1) / per;
+}
+
+inline bool split_head_dim(int32_t D) { return D == 64 || D == 128 || D == 256; }
+
+// Sum over the LPR lanes of a row group (lanes LPR g .. LPR g + LPR - 1).
+template <int LPR>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (LPR == 16) {
+    // DPP rotates within 16-lane rows: every lane of the row gets the sum
+    int v = __builtin_bit_cast(int, x);
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false));
+    v = __builtin_bit_cast(int, x);
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false));
+    v = __builtin_bit_cast(int, x);
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x122, 0xF, 0xF, false));
+    v = __builtin_bit_cast(int, x);
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x121, 0xF, 0xF, false));
+    return x;
+  } else {
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) x += __shfl_xor(x, o);
+    return x;
+  }
+}
+
+// Sum / max over the row groups (lanes with the same lane % LPR).
+template <int LPR>
+__device__ __forceinline__ float across_groups_sum(float x) {
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1) x += __shfl_xor(x, o);
+  return x;
+}
+template <int LPR>
+__device__ __forceinline__ float across_groups_max(float x) {
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+// One wave per (query row, split).  LPR = head_dim / 8 lanes per K/V row,
+// TPS = 64 / LPR rows per wave load; lane (g = lane / LPR, c = lane % LPR)
+// holds query elements 8c .. 8c + 7 and, in step i of a 64-token chunk, token
+// chunk + TPS i + g.
+//
+// Workgroup order: a unit is (b, kv head, tq, split) and its G = Hq / Hkv
+// query heads read the same K/V rows.  Workgroups are dealt to the 8 XCDs
+// round-robin by id, so unit u goes to XCD u % 8 and its G waves take
+// consecutive slots there: the group shares one L2.
+// INT4 = true: K and V are INT4_SYM codes, dequantized as the codec's restore
+// does, (code - 8) * scale in fp32 rounded to DT (the dtype the restore would
+// write and q's dtype), so the scores see the values a decompressed tensor
+// holds.
+template <int DT>
+__device__ __forceinline__ void int4_sym_row8(uint32_t w, const float (&s)[8], float (&x)[8]) {
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    float y = ((float)__builtin_amdgcn_ubfe(w, 4 * n, 4) - 8.0f) * s[n];
+    if constexpr (DT == AMF_DTYPE_BF16) {
+      y = (float)(__bf16)y;
+    } else if constexpr (DT == AMF_DTYPE_F16) {
+      amf::keep_f32(y);
+      y = (float)(_Float16)y;
+    }
+    x[n] = y;
+  }
+}
+
+// One lane's 8 elements of a K/V row as loaded (lane c of a row group holds
+// dims 8c .. 8c + 7 of a head_dim-D row): a code word for INT4, else 16
+// (bf16/fp16) or 32 (fp32) bytes.
+template <int DT, bool INT4>
+struct RawRow {  // bf16 / fp16
+  u32x4 w;
+  static __device__ __forceinline__ RawRow load(const void* base, int64_t r, int c, int D) {
+    return RawRow{*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + r * D +
+                                                  8 * c)};
+  }
+  __device__ __forceinline__ void decode(const float (&)[8], float (&x)[8]) const {
+    amf::unpack8<DT == AMF_DTYPE_BF16>(w, x);
+  }
+};
+
+template <>
+struct RawRow<AMF_DTYPE_F32, false> {
+  f32x4 lo, hi;
+  static __device__ __forceinline__ RawRow load(const void* base, int64_t r, int c, int D) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + r * D + 8 * c);
+    return RawRow{p[0], p[1]};
+  }
+  __device__ __forceinline__ void decode(const float (&)[8], float (&x)[8]) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = lo[e];
+      x[4 + e] = hi[e];
+    }
+  }
+};
+
+template <int DT>
+struct RawRow<DT, true> {
+  uint32_t w;
+  static __device__ __forceinline__ RawRow load(const void* base, int64_t r, int c, int D) {
+    return RawRow{static_cast<const uint32_t*>(base)[r * (D / 8) + c]};
+  }
+  __device__ __forceinline__ void decode(const float (&s)[8], float (&x)[8]) const {
+    int4_sym_row8<DT>(w, s, x);
+  }
+};
+
+// Wave loads one batch keeps in flight per operand.
+template <int DT, bool INT4>
+constexpr int kBatchLoads = (!INT4 && DT == AMF_DTYPE_F32) ? 8 : 16;
+
+template <int DT, int LPR, bool INT4>
+__global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float* part,
+                                                              int64_t split_tokens,
+                                                              int64_t n_splits, int64_t units) {
+  constexpr int TPS = 64 / LPR;
+  constexpr int STEPS = LPR;  // 64-token chunk = STEPS loads of TPS rows
+  const int lane = threadIdx.x, g = lane / LPR, c = lane % LPR;
+  const int G = a.num_q_heads / a.num_kv_heads;
+  const int64_t id = blockIdx.x, slot = id / kXcds;
+  const int r = (int)(slot % G);
+  const int64_t u = (slot / G) * kXcds + id % kXcds;
+  if (u >= units) return;
+  const int64_t split = u % n_splits, rest = u / n_splits;
+  const int64_t tq = rest % a.q_len, bkv = rest / a.q_len;
+  const int hkv = (int)(bkv % a.num_kv_heads);
+  const int64_t b = bkv / a.num_kv_heads;
+  const int h = hkv * G + r;
+  const int64_t row = (b * a.num_q_heads + h) * a.q_len + tq;  // (b, h, tq) flattened
+  const int D = 8 * LPR;
+  const int64_t T = a.kv_len;
+  const int64_t t_begin = split * split_tokens, t_end = min(T, t_begin + split_tokens);
+  const int64_t kv_base = (b * a.num_kv_heads + hkv) * T;
+  const float* mrow = a.mask ? a.mask + b * a.ms0 + (int64_t)h * a.ms1 + tq * a.ms2 : nullptr;
+  const float qs = a.scale * kLog2e;
+
+  float q[8];
+  elem8<DT>(a.q, row * D + 8 * c, q);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) q[e] *= qs;
+  float ksc[8], vsc[8];  // this lane's 8 channels' scales (INT4)
+  if constexpr (INT4) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ksc[e] = (float)a.k_scales[8 * c + e];
+      vsc[e] = (float)a.v_scales[8 * c + e];
+    }
+  }
+  float m_run = -INFINITY, l_run = 0.0f;  // l_run: this lane's group's tokens
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+
+  // A batch is SB wave loads of TPS rows each; its K (and, for INT4, V)
+  // loads are all issued before the first is used.
+  constexpr int SB = STEPS < kBatchLoads<DT, INT4> ? STEPS : kBatchLoads<DT, INT4>;
+  constexpr int BT = TPS * SB;  // tokens per batch, divides 64
+  using Raw = RawRow<DT, INT4>;
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += BT) {
+    Raw kr[SB];
+    Raw vr[INT4 ? SB : 1];
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      const int64_t t = t0 + TPS * i + g;
+      kr[i] = Raw::load(a.k, kv_base + (t < t_end ? t : t_begin), c, D);
+    }
+    if constexpr (INT4) {
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const int64_t t = t0 + TPS * i + g;
+        vr[i] = Raw::load(a.v, kv_base + (t < t_end ? t : t_begin), c, D);
+      }
+    }
+    float mk[SB];
+    if (mrow) {
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const int64_t t = t0 + TPS * i + g;
+        mk[i] = mrow[(t < t_end ? t : t_begin) * a.ms3];
+      }
+    }
+    float sc[SB];
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      float x[8];
+      kr[i].decode(ksc, x);
+      float d = q[0] * x[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) d = fmaf(q[e], x[e], d);
+      d = group_sum<LPR>(d);
+      if (mrow) d = fmaf(mk[i], kLog2e, d);
+      sc[i] = t0 + TPS * i + g < t_end ? d : -INFINITY;
+    }
+    float mc = sc[0];
+#pragma unroll
+    for (int i = 1; i < SB; ++i) mc = fmaxf(mc, sc[i]);
+    mc = across_groups_max<LPR>(mc);
+    const float m_new = fmaxf(m_run, mc);
+    if (m_new == -INFINITY) continue;  // every score so far is -inf (wave-uniform)
+    const float alpha = exp2f(m_run - m_new);
+    l_run *= alpha;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+    if constexpr (!INT4) {
+      // dense V: loaded after the scores, all SB loads in flight together
+      Raw vd[SB];
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const int64_t t = t0 + TPS * i + g;
+        vd[i] = Raw::load(a.v, kv_base + (t < t_end ? t : t_begin), c, D);
+      }
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const float p = sc[i] == -INFINITY ? 0.0f : exp2f(sc[i] - m_new);
+        l_run += p;
+        float x[8];
+        vd[i].decode(vsc, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, x[e], acc[e]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const float p = sc[i] == -INFINITY ? 0.0f : exp2f(sc[i] - m_new);
+        l_run += p;
+        float x[8];
+        vr[i].decode(vsc, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, x[e], acc[e]);
+      }
+    }
+    m_run = m_new;
+  }
+  // the row groups hold disjoint tokens: add them up
+  l_run = across_groups_sum<LPR>(l_run);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = across_groups_sum<LPR>(acc[e]);
+  float* pr = part + (row * n_splits + split) * (int64_t)(D + kPartPad);
+  if (g == 0) {
+    *reinterpret_cast<f32x4*>(pr + 8 * c) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4*>(pr + 8 * c + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+  }
+  if (lane == 0) {
+    pr[D] = m_run;
+    pr[D + 1] = l_run;
+  }
+}
+
+// One wave per query row: out = sum_k 2^(m_k - M) acc_k / sum_k 2^(m_k - M) l_k.
+// The split weights go through LDS; lane (phase, quad) then sums the f32x4
+// quad `quad` of the splits phase, phase + P, ... (P = 256 / D phases), with
+// the loads of four splits in flight, and the phases are added by shuffles.
+constexpr int kMaxSplits = 4096;
+static_assert(kSplitWaves <= kMaxSplits, "dense_splits gives at most kSplitWaves splits");
+
+template <int OUT_DT, int D>
+__global__ __launch_bounds__(64) void dense_attn_merge_kernel(AttnArgs a, const float* part,
+                                                              int64_t n_splits) {
+  constexpr int Q = D / 4, P = 64 / Q, STRIDE = D + kPartPad;
+  __shared__ float f_s[kMaxSplits];
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int ns = (int)n_splits;
+  const float* pr = part + row * n_splits * (int64_t)STRIDE;
+  float M = -INFINITY;
+  for (int k = lane; k < ns; k += 64) M = fmaxf(M, pr[(int64_t)k * STRIDE + D]);
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  float den = 0.0f;
+  for (int k = lane; k < ns; k += 64) {
+    const float mk = pr[(int64_t)k * STRIDE + D];
+    const float f = (M == -INFINITY || mk == -INFINITY) ? 0.0f : exp2f(mk - M);
+    den = fmaf(pr[(int64_t)k * STRIDE + D + 1], f, den);
+    f_s[k] = f;
+  }
+  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
+  __syncthreads();
+  const int quad = lane % Q, phase = lane / Q;
+  f32x4 o4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  int k = phase;
+  for (; k + 3 * P < ns; k += 4 * P) {
+    f32x4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      x[u] = *reinterpret_cast<const f32x4*>(pr + (int64_t)(k + u * P) * STRIDE + 4 * quad);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float f = f_s[k + u * P];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = fmaf(x[u][e], f, o4[e]);
+    }
+  }
+  for (; k < ns; k += P) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(pr + (int64_t)k * STRIDE + 4 * quad);
+    const float f = f_s[k];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o4[e] = fmaf(x[e], f, o4[e]);
+  }
+#pragma unroll
+  for (int o = Q; o < 64; o <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o4[e] += __shfl_xor(o4[e], o);
+  }
+  // a row whose scores are all -inf: 0 / 0 = NaN, as softmax gives
+  if (phase == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_out<OUT_DT>(a.out, row * D + 4 * quad + e, o4[e] / den);
+  }
+}
+
+// Workgroups of the split launch: units rounded up to the XCD count, times G.
+inline int64_t split_grid(int64_t rows, int64_t n_splits, int32_t num_q_heads,
+                          int32_t num_kv_heads, int64_t* units) {
+  const int64_t G = num_q_heads / num_kv_heads;
+  *units = rows / G * n_splits;
+  return (*units + kXcds - 1) / kXcds * kXcds * G;
+}
+
+template <int DT, bool INT4>
+void launch_split(const AttnArgs& a, int32_t out_dtype, int64_t rows, float* part,
+                  int64_t split_tokens, int64_t n_splits, hipStream_t st) {
+  int64_t units = 0;
+  const dim3 grid((unsigned)split_grid(rows, n_splits, a.num_q_heads, a.num_kv_heads, &units));
+  if (a.head_dim == 64)
+    dense_attn_split_kernel<DT, 8, INT4><<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits,
+                                                               units);
+  else if (a.head_dim == 128)
+    dense_attn_split_kernel<DT, 16, INT4><<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits,
+                                                                units);
+  else
+    dense_attn_split_kernel<DT, 32, INT4><<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits,
+                                                                units);
+  const dim3 mgrid((unsigned)rows);
+#define AMF_MERGE(OUT)                                                                   \
+  if (a.head_dim == 64)                                                                  \
+    dense_attn_merge_kernel<OUT, 64><<<mgrid, 64, 0, st>>>(a, part, n_splits);           \
+  else if (a.head_dim == 128)                                                            \
+    dense_attn_merge_kernel<OUT, 128><<<mgrid, 64, 0, st>>>(a, part, n_splits);          \
+  else                                                                                   \
+    dense_attn_merge_kernel<OUT, 256><<<mgrid, 64, 0, st>>>(a, part, n_splits)
+  if (out_dtype == AMF_DTYPE_F32) {
+    AMF_MERGE(AMF_DTYPE_F32);
+  } else if (out_dtype == AMF_DTYPE_BF16) {
+    AMF_MERGE(AMF_DTYPE_BF16);
+  } else {
+    AMF_MERGE(AMF_DTYPE_F16);
+  }
+#undef AMF_MERGE
+}
+
 template <int DT, int OUT_DT>
 void launch_typed(const AttnArgs& a, bool vec8, int64_t rows, hipStream_t st) {
   if (vec8)
@@ -217,18 +607,11 @@ bool is_dtype(int32_t t) {
   return t == AMF_DTYPE_F16 || t == AMF_DTYPE_F32 || t == AMF_DTYPE_BF16;
 }
 
-}  // namespace
-
-extern "C" int amf_dense_attn(const void* q, const void* k, const void* v, int32_t dtype,
-                              const float* mask, int64_t mask_stride_b, int64_t mask_stride_h,
-                              int64_t mask_stride_q, int64_t mask_stride_t, void* out,
-                              int32_t out_dtype, int64_t batch, int32_t num_q_heads,
-                              int32_t num_kv_heads, int64_t q_len, int64_t kv_len,
-                              int32_t head_dim, float softmax_scale, void* stream) {
+// Shape and dtype checks shared by the dense and INT4_SYM entry points.
+int check_attn_args(const char* who, int32_t dtype, int32_t out_dtype, int64_t batch,
+                    int32_t num_q_heads, int32_t num_kv_heads, int64_t q_len, int64_t kv_len,
+                    int32_t head_dim) {
   using namespace amf;
-  const char* who = "amf_dense_attn";
-  if (!q || !out || (kv_len > 0 && (!k || !v)))
-    return fail(AMF_ERR_INVALID_ARG, "%s: null q/k/v/out", who);
   if (!is_dtype(dtype) || !is_dtype(out_dtype))
     return fail(AMF_ERR_INVALID_ARG, "%s: bad dtype %d / out_dtype %d", who, dtype, out_dtype);
   if (batch < 0 || q_len < 0 || kv_len < 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
@@ -240,23 +623,131 @@ extern "C" int amf_dense_attn(const void* q, const void* k, const void* v, int32
                 num_kv_heads);
   if (head_dim <= 0 || head_dim > kMaxD)
     return fail(AMF_ERR_UNSUPPORTED, "%s: head_dim %d outside [1, %d]", who, head_dim, kMaxD);
+  if (batch > 0x7FFFFFFF || q_len > 0x7FFFFFFF ||
+      (batch > 0 && q_len > 0x7FFFFFFF / batch) || batch * q_len * num_q_heads > 0x7FFFFFFF)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: batch %lld x %d heads x %lld rows exceed one launch",
+                who, (long long)batch, num_q_heads, (long long)q_len);
+  return ok();
+}
+
+}  // namespace
+
+extern "C" int64_t amf_dense_attn_workspace_bytes(int64_t batch, int32_t num_q_heads,
+                                                  int64_t q_len, int64_t kv_len,
+                                                  int32_t head_dim) {
+  if (batch <= 0 || num_q_heads <= 0 || q_len <= 0 || kv_len <= 0 || !split_head_dim(head_dim) ||
+      batch > 0x7FFFFFFF || q_len > 0x7FFFFFFF)
+    return 0;
   const int64_t rows = batch * num_q_heads * q_len;
-  if (rows > 0x7FFFFFFF)
-    return fail(AMF_ERR_UNSUPPORTED, "%s: %lld query rows exceed one launch", who,
-                (long long)rows);
+  if (rows > 0x7FFFFFFF) return 0;
+  int64_t n_splits = 1, split_tokens = 64;
+  dense_splits(rows, kv_len, &n_splits, &split_tokens);
+  // The split launch has at most rows * n_splits + 8 * num_q_heads
+  // workgroups; a shape beyond one launch takes the single-pass kernel.
+  if (rows > (0x7FFFFFFF - kXcds * num_q_heads) / n_splits) return 0;
+  return rows * n_splits * (int64_t)(head_dim + kPartPad) * (int64_t)sizeof(float);
+}
+
+extern "C" int amf_dense_attn(const void* q, const void* k, const void* v, int32_t dtype,
+                              const float* mask, int64_t mask_stride_b, int64_t mask_stride_h,
+                              int64_t mask_stride_q, int64_t mask_stride_t, void* out,
+                              int32_t out_dtype, int64_t batch, int32_t num_q_heads,
+                              int32_t num_kv_heads, int64_t q_len, int64_t kv_len,
+                              int32_t head_dim, float softmax_scale, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+  using namespace amf;
+  const char* who = "amf_dense_attn";
+  if (!q || !out || (kv_len > 0 && (!k || !v)))
+    return fail(AMF_ERR_INVALID_ARG, "%s: null q/k/v/out", who);
+  int rc = check_attn_args(who, dtype, out_dtype, batch, num_q_heads, num_kv_heads, q_len,
+                           kv_len, head_dim);
+  if (rc) return rc;
+  const int64_t rows = batch * num_q_heads * q_len;
   if (rows == 0) return ok();
   const int esize = dtype == AMF_DTYPE_F32 ? 4 : 2;
   const bool vec8 = head_dim % 8 == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 &&
                     ((int64_t)head_dim * esize) % 16 == 0;
   AttnArgs a{q, k, v, mask, mask_stride_b, mask_stride_h, mask_stride_q, mask_stride_t, out,
              batch, num_q_heads, num_kv_heads, q_len, kv_len, head_dim,
-             softmax_scale};
+             softmax_scale, nullptr, nullptr};
   hipStream_t st = as_stream(stream);
+  const int64_t need =
+      amf_dense_attn_workspace_bytes(batch, num_q_heads, q_len, kv_len, head_dim);
+  if (need > 0 && vec8 && ((uintptr_t)q % 16) == 0 && workspace && workspace_bytes >= need &&
+      ((uintptr_t)workspace % 16) == 0) {
+    int64_t n_splits = 1, split_tokens = 64;
+    dense_splits(rows, kv_len, &n_splits, &split_tokens);
+    float* part = static_cast<float*>(workspace);
+    if (dtype == AMF_DTYPE_F32)
+      launch_split<AMF_DTYPE_F32, false>(a, out_dtype, rows, part, split_tokens, n_splits, st);
+    else if (dtype == AMF_DTYPE_BF16)
+      launch_split<AMF_DTYPE_BF16, false>(a, out_dtype, rows, part, split_tokens, n_splits, st);
+    else
+      launch_split<AMF_DTYPE_F16, false>(a, out_dtype, rows, part, split_tokens, n_splits, st);
+    return check_launch(who);
+  }
   if (dtype == AMF_DTYPE_F32)
     launch_out<AMF_DTYPE_F32>(a, out_dtype, vec8, rows, st);
   else if (dtype == AMF_DTYPE_BF16)
     launch_out<AMF_DTYPE_BF16>(a, out_dtype, vec8, rows, st);
   else
     launch_out<AMF_DTYPE_F16>(a, out_dtype, vec8, rows, st);
+  return check_launch(who);
+}
+
+extern "C" int amf_int4_sym_dense_attn(const void* q, int32_t dtype, const void* k_codes,
+                                       const uint16_t* k_scales, const void* v_codes,
+                                       const uint16_t* v_scales, const float* mask,
+                                       int64_t mask_stride_b, int64_t mask_stride_h,
+                                       int64_t mask_stride_q, int64_t mask_stride_t, void* out,
+                                       int32_t out_dtype, int64_t batch, int32_t num_q_heads,
+                                       int32_t num_kv_heads, int64_t q_len, int64_t kv_len,
+                                       int32_t head_dim, float softmax_scale, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  using namespace amf;
+  const char* who = "amf_int4_sym_dense_attn";
+  if (!q || !out || (kv_len > 0 && (!k_codes || !v_codes || !k_scales || !v_scales)))
+    return fail(AMF_ERR_INVALID_ARG, "%s: null q/codes/scales/out", who);
+  int rc = check_attn_args(who, dtype, out_dtype, batch, num_q_heads, num_kv_heads, q_len,
+                           kv_len, head_dim);
+  if (rc) return rc;
+  if (!split_head_dim(head_dim))
+    return fail(AMF_ERR_UNSUPPORTED, "%s: head_dim %d (64, 128 or 256 only)", who, head_dim);
+  if (((uintptr_t)q % 16) != 0 || ((uintptr_t)k_codes % 4) != 0 || ((uintptr_t)v_codes % 4) != 0 ||
+      ((uintptr_t)k_scales % 2) != 0 || ((uintptr_t)v_scales % 2) != 0)
+    return fail(AMF_ERR_INVALID_ARG, "%s: q must be 16-byte, codes 4-byte aligned", who);
+  const int64_t rows = batch * num_q_heads * q_len;
+  if (rows == 0) return ok();
+  AttnArgs a{q, k_codes, v_codes, mask, mask_stride_b, mask_stride_h, mask_stride_q,
+             mask_stride_t, out, batch, num_q_heads, num_kv_heads, q_len, kv_len, head_dim,
+             softmax_scale, reinterpret_cast<const _Float16*>(k_scales),
+             reinterpret_cast<const _Float16*>(v_scales)};
+  hipStream_t st = as_stream(stream);
+  if (kv_len == 0) {  // an empty softmax: zeros, no K/V read
+    if (dtype == AMF_DTYPE_F32)
+      launch_out<AMF_DTYPE_F32>(a, out_dtype, false, rows, st);
+    else if (dtype == AMF_DTYPE_BF16)
+      launch_out<AMF_DTYPE_BF16>(a, out_dtype, false, rows, st);
+    else
+      launch_out<AMF_DTYPE_F16>(a, out_dtype, false, rows, st);
+    return check_launch(who);
+  }
+  const int64_t need =
+      amf_dense_attn_workspace_bytes(batch, num_q_heads, q_len, kv_len, head_dim);
+  if (need == 0)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: %lld query rows exceed one launch", who,
+                (long long)rows);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 16) != 0)
+    return fail(AMF_ERR_WORKSPACE, "%s: needs %lld workspace bytes (16-byte aligned)", who,
+                (long long)need);
+  int64_t n_splits = 1, split_tokens = 64;
+  dense_splits(rows, kv_len, &n_splits, &split_tokens);
+  float* part = static_cast<float*>(workspace);
+  if (dtype == AMF_DTYPE_F32)
+    launch_split<AMF_DTYPE_F32, true>(a, out_dtype, rows, part, split_tokens, n_splits, st);
+  else if (dtype == AMF_DTYPE_BF16)
+    launch_split<AMF_DTYPE_BF16, true>(a, out_dtype, rows, part, split_tokens, n_splits, st);
+  else
+    launch_split<AMF_DTYPE_F16, true>(a, out_dtype, rows, part, split_tokens, n_splits, st);
   return check_launch(who);
 }

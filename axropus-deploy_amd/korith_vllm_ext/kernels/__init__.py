@@ -5,6 +5,7 @@ from __future__ import annotations
 from .dispatch import (
     KERNEL_DISPATCH,
     dense_attention,
+    int4_sym_attention,
     dispatch_kernel,
     fallback_fp16_kernel,
     get_current_sm_version,
@@ -17,6 +18,7 @@ from .dispatch import (
 __all__ = [
     "KERNEL_DISPATCH",
     "dense_attention",
+    "int4_sym_attention",
     "dispatch_kernel",
     "fallback_fp16_kernel",
     "get_current_sm_version",

@@ -9,7 +9,9 @@ Every kernel registered here runs on the GPU through libamf_hip.so:
 
 * hip_decode_attention(q, k, v, scale=None, mask=None, *, block_tables=...,
   context_lens=...) is the paged GQA INT4 decode (amf_int4_paged_decode_attn)
-  when a block table is given, and dense attention (amf_dense_attn) otherwise.
+  when a block table is given, and dense attention otherwise: straight from
+  the codes for int4_sym CompressedKV K/V (amf_int4_sym_dense_attn), else
+  over the restored K/V (amf_dense_attn).
 * fallback_fp16_kernel keeps the reference's name and signature
   (dispatch.py:117-143): decompress compressed K/V with the HIP codecs, then
   softmax(q k^T * scale + mask) v with the HIP dense-attention kernel, in fp32,
@@ -146,9 +148,82 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Op
         m4 = mask.to(device=q.device, dtype=torch.float32).expand(*lead, Hq, Tq, T)
         m4 = m4.reshape(B, Hq, Tq, T)
         mptr, ms = m4.data_ptr(), tuple(m4.stride())
+    # split-K scratch (per-split softmax partials), 0 bytes when the shape
+    # takes the single-pass kernel
+    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Tq, T, D))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=q.device) if wsb else None
     amf_hip.call("amf_dense_attn", qc.data_ptr(), k.data_ptr(), v.data_ptr(),
                  amf_hip.dtype_tag(q.dtype), mptr, ms[0], ms[1], ms[2], ms[3], out.data_ptr(),
                  amf_hip.dtype_tag(out.dtype), B, Hq, Hkv, Tq, T, D, float(scale),
+                 ws.data_ptr() if ws is not None else None, wsb,
+                 amf_hip.stream_handle(q.device))
+    return out
+
+
+_FUSED_HEAD_DIMS = (64, 128, 256)
+
+
+def _int4_sym_operands(c: Any, q: torch.Tensor) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+    """(codes, scales) of an int4_sym CompressedKV that the fused kernel can
+    read in place: codes uint8 [*lead, Hkv, T, D/2] contiguous, scales fp16
+    [D], both on q's device, lead dims equal to q's; None otherwise."""
+    if not isinstance(c, CompressedKV) or c.format != FMT_INT4_SYM:
+        return None
+    shape = tuple(int(d) for d in c.shape)
+    if len(shape) != q.dim() or shape[:-3] != tuple(q.shape[:-3]) or shape[-1] != q.shape[-1]:
+        return None
+    D = shape[-1]
+    codes, scales = c.data, c.scales
+    if not isinstance(codes, torch.Tensor) or not isinstance(scales, torch.Tensor):
+        return None
+    if (codes.dtype != torch.uint8 or tuple(codes.shape) != shape[:-1] + (D // 2,)
+            or not codes.is_contiguous() or codes.device != q.device):
+        return None
+    if (scales.dtype != torch.float16 or scales.numel() != D or not scales.is_contiguous()
+            or scales.device != q.device):
+        return None
+    return codes, scales
+
+
+def int4_sym_attention(q: torch.Tensor, k: Any, v: Any, scale: Optional[float],
+                       mask: Optional[torch.Tensor], out_dtype: Optional[torch.dtype] = None
+                       ) -> Optional[torch.Tensor]:
+    """softmax(q k^T * scale + mask) v straight from int4_sym CompressedKV
+    K and V (amf_int4_sym_dense_attn): the same values decompress_to(q.dtype)
+    would restore, without writing them out.  None when k/v are not int4_sym
+    CompressedKV of q's layout or the head dim is not 64/128/256 (the caller
+    then restores and runs dense_attention)."""
+    if q.dtype not in _DTYPES or q.dim() < 3 or q.shape[-1] not in _FUSED_HEAD_DIMS:
+        return None
+    ko, vo = _int4_sym_operands(k, q), _int4_sym_operands(v, q)
+    if ko is None or vo is None or tuple(k.shape) != tuple(v.shape):
+        return None
+    Hq, Tq, D = q.shape[-3:]
+    Hkv, T = int(k.shape[-3]), int(k.shape[-2])
+    if Hq % Hkv != 0:
+        return None
+    amf_hip.require_device_tensor(q, "int4_sym attention q")
+    B = 1
+    for d in q.shape[:-3]:
+        B *= int(d)
+    qc = q.contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+    mptr, ms = 0, (0, 0, 0, 0)
+    m4 = None
+    if mask is not None:
+        m4 = mask.to(device=q.device, dtype=torch.float32).expand(*q.shape[:-3], Hq, Tq, T)
+        m4 = m4.reshape(B, Hq, Tq, T)
+        mptr, ms = m4.data_ptr(), tuple(m4.stride())
+    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Tq, T, D))
+    if T > 0 and wsb == 0:
+        return None  # beyond one split launch: the restoring path takes it
+    ws = torch.empty(wsb, dtype=torch.uint8, device=q.device) if wsb else None
+    amf_hip.call("amf_int4_sym_dense_attn", qc.data_ptr(), amf_hip.dtype_tag(q.dtype),
+                 ko[0].data_ptr(), ko[1].data_ptr(), vo[0].data_ptr(), vo[1].data_ptr(), mptr,
+                 ms[0], ms[1], ms[2], ms[3], out.data_ptr(), amf_hip.dtype_tag(out.dtype), B, Hq,
+                 Hkv, Tq, T, D, float(scale), ws.data_ptr() if ws is not None else None, wsb,
                  amf_hip.stream_handle(q.device))
     return out
 
@@ -162,6 +237,9 @@ def fallback_fp16_kernel(q: torch.Tensor, k_compressed: Any, v_compressed: Any, 
     q [batch, heads, q_tokens, head_dim]; k/v a CompressedKV or a tensor
     [batch, kv_heads, kv_tokens, head_dim]; scale defaults to 1/sqrt(head_dim);
     mask is additive.  Returns q's shape and dtype."""
+    fused = int4_sym_attention(q, k_compressed, v_compressed, scale, mask)
+    if fused is not None:
+        return fused
     k = _to_tensor(k_compressed, q)
     v = _to_tensor(v_compressed, q)
     return dense_attention(q, k, v, scale, mask)
@@ -275,9 +353,9 @@ def hip_decode_attention(q: torch.Tensor, k: Any, v: Any = None, scale: Optional
         return paged_int4_decode(q, k, block_tables, context_lens, scale=scale,
                                  max_context_len=max_context_len, out=out, out_dtype=out_dtype,
                                  algo=algo, workspace=workspace)
-    kt = _to_tensor(k, q)
-    vt = _to_tensor(v, q)
-    res = dense_attention(q, kt, vt, scale, mask, out_dtype)
+    res = int4_sym_attention(q, k, v, scale, mask, out_dtype)
+    if res is None:
+        res = dense_attention(q, _to_tensor(k, q), _to_tensor(v, q), scale, mask, out_dtype)
     if out is not None:
         out.copy_(res)
         return out
@@ -310,6 +388,7 @@ __all__ = [
     "GFX950_VERSION",
     "KERNEL_DISPATCH",
     "dense_attention",
+    "int4_sym_attention",
     "dispatch_kernel",
     "fallback_fp16_kernel",
     "get_current_sm_version",

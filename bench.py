@@ -53,6 +53,7 @@ for _p in (ROOT, os.path.join(ROOT, "axropus-deploy_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
+import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 METRIC = "KV restore GB/s (FP8/INT4 dequant+scatter); INT4 decode-attn tok/s; 1 GPU"
@@ -464,6 +465,53 @@ class ConnectorCase:
                 "slot_gather_GB/s": round(moved / slot_ms / 1e6, 1),
                 "slot_gather_frac": round(moved / slot_ms / 1e6 / HBM_PEAK_GBS, 4)}
 
+    def cpu_baseline(self, sample_layers: int = 2, min_runs: int = 3, min_seconds: float = 3.0):
+        """The reference connector's op sequence on the host for
+        `sample_layers` layers: save = flat[:, slots].clone() per layer, a
+        stack of the layers and FP8E4M3Codec.compress of each
+        (amf_kv_connector.py:409-442 and the pool insert); load =
+        decompress_to(bf16) and flat_cache[:, slots] = rows per layer
+        (:365-385).  The loaded rows are compared bit for bit with the
+        GPU connector's warm load; call after run()."""
+        from oracle import codecs as oc
+
+        torch.cuda.synchronize()
+        L, H, D, T = sample_layers, self.heads, self.head_dim, self.tokens
+        src = [self.cache[l].cpu() for l in range(L)]
+        dst = [torch.zeros_like(c) for c in src]
+        cold = torch.tensor([b * 16 + j for b in self.cold[:self.pages] for j in range(16)])
+        warm = torch.tensor([b * 16 + j for b in self.warm[:self.pages] for j in range(16)])
+        gpu_rows = [self.target[l].reshape(2, -1, H, D)[:, warm.to(DEV)].cpu() for l in range(L)]
+        saved = [None] * L
+        per_layer = self.algo_bytes() // self.layers
+
+        def save():
+            kv = [c.reshape(2, -1, H, D)[:, cold].clone() for c in src]
+            stacked = torch.stack(kv, dim=0)
+            for l in range(L):
+                saved[l] = oc.fp8_tensor_compress(stacked[l])
+
+        def load():
+            for l in range(L):
+                codes, scale = saved[l]
+                rows = oc.fp8_tensor_decompress(codes, scale, torch.bfloat16).reshape(2, T, H * D)
+                dst[l].reshape(2, -1, H * D)[:, warm] = rows
+
+        def timed() -> dict:
+            ts, ns, _ = cpu_time(save, min_runs, min_seconds)
+            tl, nl, _ = cpu_time(load, min_runs, min_seconds)
+            same = all(bits_equal(dst[l].reshape(2, -1, H, D)[:, warm], gpu_rows[l])
+                       for l in range(L))
+            return {"save_GB/s": round(per_layer * L / ts / 1e9, 3),
+                    "load_GB/s": round(per_layer * L / tl / 1e9, 3),
+                    "save_ms_all_layers": round(ts * 1e3 * self.layers / L, 2),
+                    "load_ms_all_layers": round(tl * 1e3 * self.layers / L, 2),
+                    "sample": f"{L} of {self.layers} layers ({T} tokens), median of {ns} / {nl} "
+                              f"runs; all-layer times scaled linearly",
+                    "parity_vs_gpu": "bit-exact" if same else "MISMATCH"}
+
+        return timed
+
     def free(self):
         del self.conn, self.cache, self.target
         torch.cuda.empty_cache()
@@ -597,6 +645,87 @@ class DecodeCase:
                     "sample": f"{sample_seqs} of {batch} sequences ({sum_ctx} context "
                               f"tokens), median of {runs} runs ({total:.1f} s)",
                     "gpu_vs_cpu_fallback": {k: float(f"{v:.3e}") for k, v in err.items()}}
+
+        return timed
+
+
+class PositionalDecodeCase:
+    """The reference's positional decode contract, int4_decode_attention(q, k,
+    v) (int4_decode_attention.py:6-9 -> dispatch.py:117-143): K and V as
+    int4_sym CompressedKV (per-channel INT4, the dispatch key) of [batch,
+    Hkv, tokens, D] bf16, q [batch, Hq, 1, D].  Here the call decompresses K
+    and V with the HIP codec and runs the HIP dense-attention kernel (GQA);
+    the reference materializes bf16 K/V the same way and then runs
+    matmul -> softmax -> matmul in bf16."""
+
+    def __init__(self, batch=4, tokens=8192, q_heads=32, kv_heads=8, head_dim=128, seed=21):
+        from korith_vllm_ext.codecs import get_codec
+
+        g = torch.Generator().manual_seed(seed)
+        B, T, Hq, H, D = batch, tokens, q_heads, kv_heads, head_dim
+        self.B, self.T, self.Hq, self.H, self.D = B, T, Hq, H, D
+        self.q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16).to(DEV)
+        k = device_kv((B, H, T, D), D, seed * 31 + 1)
+        v = device_kv((B, H, T, D), D, seed * 31 + 2)
+        codec = get_codec("int4_sym")
+        self.kc, self.vc = codec.compress(k), codec.compress(v)
+        del k, v
+        torch.cuda.synchronize()
+
+    def launch(self):
+        from korith_vllm_ext.int4_decode_attention import int4_decode_attention
+
+        self.out = int4_decode_attention(self.q, self.kc, self.vc)
+
+    @property
+    def algo_bytes(self) -> int:
+        """The compressed K and V read (codes and scales) plus q and out."""
+        return self.kc.nbytes() + self.vc.nbytes() + 2 * 2 * self.B * self.Hq * self.D
+
+    def cpu_fallback(self, min_runs: int = 3, min_seconds: float = 3.0):
+        """The reference path on the host for sequence 0: decompress K and V
+        (INT4PerChannelCodec.decompress_to restated), repeat the KV heads
+        for the GQA group, then fallback_fp16_kernel's matmul -> softmax ->
+        matmul in bf16; the GPU output's distance from it and from float64
+        attention over the same dequantized K/V is reported."""
+        from oracle import attention as oatt
+        from oracle import codecs as oc
+
+        torch.cuda.synchronize()
+        R = self.Hq // self.H
+        shape = tuple(self.kc.shape)
+        kd, ks = self.kc.data.cpu(), self.kc.scales.cpu()
+        vd, vs = self.vc.data.cpu(), self.vc.scales.cpu()
+        q = self.q.cpu()
+        gpu = self.out.float().cpu()
+        res = {}
+
+        def run():
+            k = oc.int4_channel_decompress(kd, ks, shape, torch.bfloat16)[:1]
+            v = oc.int4_channel_decompress(vd, vs, shape, torch.bfloat16)[:1]
+            k = k.repeat_interleave(R, dim=1)
+            v = v.repeat_interleave(R, dim=1).contiguous()
+            res["fb"] = oatt.fallback_attention(q[:1], k, v)
+
+        def timed() -> dict:
+            t, runs, total = cpu_time(run, min_runs, min_seconds)
+            k32 = oc.int4_channel_decompress(kd, ks, shape, torch.float32)[0].double().numpy()
+            v32 = oc.int4_channel_decompress(vd, vs, shape, torch.float32)[0].double().numpy()
+            qq = q[0, :, 0].double().numpy()
+            f64 = np.empty((self.Hq, self.D))
+            for h in range(self.Hq):
+                sc = k32[h // R] @ qq[h] / math.sqrt(self.D)
+                p_ = np.exp(sc - sc.max())
+                f64[h] = (p_ / p_.sum()) @ v32[h // R]
+            f64t = torch.from_numpy(f64).float()
+            kv_bytes = self.algo_bytes // self.B
+            return {"GB/s": round(kv_bytes / t / 1e9, 3),
+                    "kv_tok_per_s": round(self.T / t, 1), "seconds": round(t, 4),
+                    "sample": f"sequence 0 of {self.B} ({self.T} tokens), median of {runs} runs "
+                              f"({total:.1f} s)",
+                    "gpu_vs_cpu_fallback": attn_errors(gpu[0, :, 0], res["fb"][0, :, 0].float()),
+                    "gpu_vs_f64": attn_errors(gpu[0, :, 0], f64t),
+                    "cpu_fallback_vs_f64": attn_errors(res["fb"][0, :, 0].float(), f64t)}
 
         return timed
 
@@ -786,6 +915,91 @@ class AmfkCase:
                 "file_dir": os.path.dirname(self.dir),
                 "parity": "bit-exact" if same else "MISMATCH"}
 
+    def cpu_baseline(self, min_runs: int = 3, min_seconds: float = 3.0):
+        """The reference's AMFK op sequence on the host, for the whole
+        workload: save = per layer k_all[ids].contiguous() / v_all[ids], the
+        header, layer table and payload bytes, one file write and a rename
+        (amf_kv_manager.py:305-378); restore = read the file, parse header and
+        table, per layer k_all[ids] = the payload's pages (:406-533).  bf16
+        pages go through their int16 view (the reference's .numpy() refuses
+        bf16).  The saved file is compared byte for byte with the GPU path's,
+        the restored pages with the GPU's; call after run()."""
+        import struct
+        import tempfile
+
+        from korith_vllm_ext import amf_kv_manager as akm
+
+        raw = self.raw
+        torch.cuda.synchronize()
+        src = [c.cpu() for c in raw.src]
+        dst = [torch.zeros_like(c) for c in src]
+        gi, si = raw.ids_g[0].long(), raw.ids_s[0].long()
+        key = self.save_mgr.compute_amf_key(self.toks)
+        gpu_file = self.save_mgr._kv_filename(key).read_bytes()
+        gpu_dst = [c[:, si.to(DEV)].cpu() for c in raw.dst]
+        tmpdir = tempfile.mkdtemp(prefix="amfk_cpu_", dir=os.path.dirname(self.dir))
+        path = os.path.join(tmpdir, "snapshot.kv")
+        n_tok = len(self.toks)
+        hfmt, lfmt = akm._HEADER_FMT, akm._LAYER_FMT
+
+        def save():
+            ks, vs = [], []
+            for c in src:
+                ks.append(c[0][gi].contiguous())
+                vs.append(c[1][gi].contiguous())
+            infos, total = [], 0
+            for k, v in zip(ks, vs):
+                kb, vb = k.numel() * k.element_size(), v.numel() * v.element_size()
+                infos.append((total, kb, total + kb, vb))
+                total += kb + vb
+            head = struct.pack(hfmt, akm._AMFK_MAGIC, akm._AMFK_VERSION, len(src), n_tok,
+                               ks[0].shape[-3], ks[0].shape[-1],
+                               akm._DTYPE_TAG.get(ks[0].dtype, 0), 0, total,
+                               key["model_hash"], key["prefix_hash"])
+            tbl = b"".join(struct.pack(lfmt, *i) for i in infos)
+            payload = bytearray(total)
+            mv = memoryview(payload)
+            for (ko, kb, vo, vb), k, v in zip(infos, ks, vs):
+                mv[ko:ko + kb] = k.view(torch.int16).numpy().tobytes()
+                mv[vo:vo + vb] = v.view(torch.int16).numpy().tobytes()
+            with open(path + ".tmp", "wb") as f:
+                f.write(head + tbl + bytes(payload))
+            os.replace(path + ".tmp", path)
+
+        def restore():
+            with open(path, "rb") as f:
+                data = f.read()
+            n_layers = struct.unpack_from(hfmt, data, 0)[2]
+            base = struct.calcsize(hfmt)
+            pay = base + n_layers * struct.calcsize(lfmt)
+            for l in range(n_layers):
+                ko, kb, vo, vb = struct.unpack_from(lfmt, data, base + l * struct.calcsize(lfmt))
+                shape = (len(si),) + tuple(dst[l].shape[2:])
+                k = torch.from_numpy(np.frombuffer(data, np.int16, kb // 2, pay + ko).copy())
+                v = torch.from_numpy(np.frombuffer(data, np.int16, vb // 2, pay + vo).copy())
+                dst[l][0][si] = k.view(torch.bfloat16).reshape(shape)
+                dst[l][1][si] = v.view(torch.bfloat16).reshape(shape)
+
+        payload_bytes = len(gpu_file) - 56 - 32 * raw.L
+
+        def timed() -> dict:
+            import shutil
+
+            ts, ns, _ = cpu_time(save, min_runs, min_seconds)
+            tr, nr, _ = cpu_time(restore, min_runs, min_seconds)
+            with open(path, "rb") as f:
+                same_file = f.read() == gpu_file
+            same_pages = all(bits_equal(dst[l][:, si], gpu_dst[l]) for l in range(raw.L))
+            shutil.rmtree(tmpdir, ignore_errors=True)
+            return {"save_GB/s": round(payload_bytes / ts / 1e9, 3),
+                    "restore_GB/s": round(payload_bytes / tr / 1e9, 3),
+                    "save_ms": round(ts * 1e3, 3), "restore_ms": round(tr * 1e3, 3),
+                    "sample": f"the whole workload, file in {os.path.dirname(self.dir)}, "
+                              f"median of {ns} / {nr} runs",
+                    "parity_vs_gpu": "bit-exact" if same_file and same_pages else "MISMATCH"}
+
+        return timed
+
     def free(self):
         import shutil
 
@@ -910,6 +1124,23 @@ def run_profile(name: str, steps: int, warmup: int) -> int:
         t = time_launches(case.launch.launch, steps, warmup)
         log(f"{name}: {t.leg(case.algo_bytes)}")
         return 0
+    if name == "positional_decode":
+        case = PositionalDecodeCase()
+        t = time_launches(case.launch, steps, warmup)
+        log(f"{name}: {t.leg(case.algo_bytes)}")
+        return 0
+    if name == "dense_decode":
+        # amf_dense_attn alone on the restored bf16 K/V of the positional case
+        from korith_vllm_ext.codecs import get_codec
+        from korith_vllm_ext.kernels import dense_attention
+
+        case = PositionalDecodeCase()
+        codec = get_codec("int4_sym")
+        kd = codec.decompress_to(case.kc, torch.bfloat16)
+        vd = codec.decompress_to(case.vc, torch.bfloat16)
+        t = time_launches(lambda: dense_attention(case.q, kd, vd, None, None), steps, warmup)
+        log(f"{name}: {t.leg(2 * kd.numel() * 2)}")
+        return 0
     if name == "decode_70b":
         case = DecodeCase(8, 64, 8, 131072, 131072, 6)
         t = time_launches(lambda: case.launch(amf_hip.DECODE_MFMA), steps, warmup)
@@ -938,7 +1169,7 @@ PROFILES = ["fp8_restore", "int4_restore", "fp8_save", "int4_save", "fp8_tensor_
             "int4_channel_save", "int4_block_save",
             "fp8_restore_70b", "decode_70b", "decode_mfma", "decode_valu", "copy", "slot_copy",
             "raw_gather", "raw_scatter", "page_scatter_8b", "page_scatter_8b_contig",
-            "fp8_restore_contig"]
+            "fp8_restore_contig", "positional_decode", "dense_decode"]
 
 
 def main() -> int:
@@ -1031,6 +1262,8 @@ def main() -> int:
             cpu_jobs.append(("c1_raw_qwen2_0_5b", "cpu", raw.cpu_baseline()))
         ak = AmfkCase(raw)
         result["amfk"] = ak.run(args.steps, args.warmup)
+        if want_cpu:
+            cpu_jobs.append(("amfk", "cpu_reference_ops", ak.cpu_baseline()))
         ak.free()
         log(f"amfk: {result['amfk']}")
         result["c1_raw_qwen2_0_5b"] = c1
@@ -1073,6 +1306,21 @@ def main() -> int:
         del dc
         torch.cuda.empty_cache()
 
+        log("positional decode: int4_decode_attention(q, k, v) on int4_sym K/V")
+        pd = PositionalDecodeCase()
+        tpd = time_launches(pd.launch, args.steps, args.warmup)
+        result["positional_decode"] = tpd.leg(
+            pd.algo_bytes, workload="positional_int4_sym_b4_8k", batch=pd.B, tokens=pd.T,
+            q_heads=pd.Hq, kv_heads=pd.H,
+            kv_tok_per_s=round(pd.B * pd.T / (tpd.median_ms * 1e-3), 1),
+            note="GB/s on the compressed K/V read; the call also writes and reads the "
+                 "decompressed bf16 K/V, as the reference's contract does")
+        log(f"positional decode: {result['positional_decode']}")
+        if want_cpu:
+            cpu_jobs.append(("positional_decode", "cpu_fallback", pd.cpu_fallback()))
+        del pd
+        torch.cuda.empty_cache()
+
         log("reference formats: restore and save at the Llama-3-8B shape")
         fmts = {}
         for fmt in ("fp8_e4m3", "int4_sym_block", "int4_sym"):
@@ -1089,6 +1337,8 @@ def main() -> int:
         cc = ConnectorCase()
         result["connector"] = cc.run(args.steps, args.warmup)
         log(f"connector: {result['connector']}")
+        if want_cpu:
+            cpu_jobs.append(("connector", "cpu_reference_ops", cc.cpu_baseline()))
         cc.free()
         del cc
         result["c5_llama3_70b"] = long_context_70b(args.steps, args.warmup, cpu_jobs, want_cpu)

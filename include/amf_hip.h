@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define AMF_ABI_VERSION 2
+#define AMF_ABI_VERSION 3
 
 /* ---- status codes ------------------------------------------------------ */
 #define AMF_OK                  0
@@ -341,6 +341,13 @@ uint64_t amf_hash_tokens(const int32_t* tokens, int64_t n_tokens);
  *   b*mask_stride_b + h*mask_stride_h + i*mask_stride_q + t*mask_stride_t
  * (element strides; 0 broadcasts).  kv_len 0 gives zeros; a row whose scores
  * are all -inf gives NaN, as softmax does.  head_dim <= 256.
+ * workspace: device scratch of workspace_bytes (16-byte aligned).  When it
+ * holds amf_dense_attn_workspace_bytes(...) bytes (non-zero only for
+ * head_dim 64, 128 or 256 and kv_len > 0) and q, k, v are 16-byte aligned,
+ * the KV tokens of each row are split over many waves (flash decoding) and
+ * merged by a second launch; otherwise (NULL, too small) one workgroup per
+ * query row runs the whole row.  Both give the same result to fp32 rounding.
+ * Calls sharing a workspace must be ordered on one stream.
  * Replaces the attention of fallback_fp16_kernel (kernels/dispatch.py:117-143),
  * which int4_decode_attention (int4_decode_attention.py:6-9) reaches for k/v
  * given as tensors or CompressedKV without a block table. */
@@ -350,7 +357,37 @@ int amf_dense_attn(const void* q, const void* k, const void* v, int32_t dtype,
                    void* out, int32_t out_dtype,
                    int64_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                    int64_t q_len, int64_t kv_len, int32_t head_dim,
-                   float softmax_scale, void* stream);
+                   float softmax_scale, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
+/* Workspace bytes amf_dense_attn needs for its split path at this shape; 0
+ * when the shape takes the single-pass path (then pass NULL, 0). */
+int64_t amf_dense_attn_workspace_bytes(int64_t batch, int32_t num_q_heads, int64_t q_len,
+                                       int64_t kv_len, int32_t head_dim);
+
+/* amf_dense_attn over INT4_SYM K and V without materialising them: k_codes
+ * and v_codes [batch, num_kv_heads, kv_len, head_dim / 2] packed codes
+ * (element 2i in the low nibble of byte i), k_scales and v_scales the fp16
+ * per-channel scales [head_dim], as an AMF_FMT_INT4_SYM codec leaves them.
+ * Each element is dequantized as the codec's restore writes it into a cache
+ * of dtype (q's dtype): (code - 8) * scale in fp32, rounded to dtype; the
+ * result equals amf_dense_attn over the restored K/V to fp32 summation
+ * order.  head_dim 64, 128 or 256; q 16-byte and codes 4-byte aligned; the
+ * workspace of amf_dense_attn_workspace_bytes (AMF_ERR_WORKSPACE without
+ * it).  kv_len 0 gives zeros.
+ * Replaces the decompress_to + fallback_fp16_kernel pair that
+ * int4_decode_attention (int4_decode_attention.py:6-9 ->
+ * kernels/dispatch.py:117-152) runs for "int4_sym" CompressedKV k/v. */
+int amf_int4_sym_dense_attn(const void* q, int32_t dtype, const void* k_codes,
+                            const uint16_t* k_scales, const void* v_codes,
+                            const uint16_t* v_scales, const float* mask,
+                            int64_t mask_stride_b, int64_t mask_stride_h,
+                            int64_t mask_stride_q, int64_t mask_stride_t,
+                            void* out, int32_t out_dtype,
+                            int64_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                            int64_t q_len, int64_t kv_len, int32_t head_dim,
+                            float softmax_scale, void* workspace, int64_t workspace_bytes,
+                            void* stream);
 
 /* ---- direct KV snapshots (AMFK blobs through pinned host staging) ----------
  * The AMFK blob: a 56-byte little-endian header

@@ -44,7 +44,7 @@ def test_header_declares_the_entry_points():
             "amf_fp8_quant_gather", "amf_fp8_dequant_scatter", "amf_int4_quant_gather",
             "amf_int4_dequant_scatter", "amf_int4_paged_decode_attn",
             "amf_int4_decode_workspace_bytes", "amf_quant_workspace_bytes",
-            "amf_dense_attn"} <= fns
+            "amf_dense_attn", "amf_dense_attn_workspace_bytes", "amf_int4_sym_dense_attn"} <= fns
 
 
 def test_every_declared_symbol_is_exported_and_bound(lib):
@@ -100,6 +100,19 @@ def _no_device():
     return not torch.cuda.is_available()
 
 
+def test_dense_attn_workspace_bytes(lib):
+    """Host-only size query: split partials of (head_dim + 4) fp32 per
+    (query row, split), splits aiming at 4096 waves, one per 64-token chunk
+    at most; 0 where the single-pass kernel runs."""
+    f = lib.amf_dense_attn_workspace_bytes
+    assert f(4, 32, 1, 8192, 128) == 128 * 32 * (128 + 4) * 4   # 32 splits of 256 tokens
+    assert f(1, 32, 1, 20000, 128) == 32 * 105 * 132 * 4        # 105 splits of 192 tokens
+    assert f(1, 2, 1, 1, 256) == 2 * 1 * 260 * 4
+    assert f(64, 64, 1, 100, 64) == 4096 * 1 * 68 * 4            # rows fill the launch alone
+    assert f(4, 32, 1, 8192, 80) == 0 and f(4, 32, 1, 0, 128) == 0
+    assert f(0, 32, 1, 8192, 128) == 0 and f(1 << 40, 32, 1, 64, 128) == 0
+
+
 # Fake addresses below are never dereferenced because every call fails
 # validation first; the guard keeps these calls off a machine with a device
 # all the same.
@@ -130,11 +143,21 @@ def test_validation_errors(lib):
                   fake, 4, fake, 1, 32, 8, 128, 16, 64, 0.0, None, 0, 0, None, None)
     assert rc == wsp and "workspace" in msg
     rc, msg = _rc(lib, "amf_dense_attn", fake, fake, fake, 2, None, 0, 0, 0, 0, fake, 2, 1, 8, 3,
-                  1, 10, 64, 0.0, None)
+                  1, 10, 64, 0.0, None, 0, None)
     assert rc == inv and "multiple" in msg
     rc, msg = _rc(lib, "amf_dense_attn", fake, fake, fake, 2, None, 0, 0, 0, 0, fake, 2, 1, 8, 8,
-                  1, 10, 512, 0.0, None)
+                  1, 10, 512, 0.0, None, 0, None)
     assert rc == uns and "head_dim" in msg
+    # INT4_SYM attention: head dims of the split kernel only, and a workspace
+    rc, msg = _rc(lib, "amf_int4_sym_dense_attn", fake, 2, fake, fake, fake, fake, None, 0, 0, 0,
+                  0, fake, 2, 1, 8, 8, 1, 10, 80, 0.0, None, 0, None)
+    assert rc == uns and "head_dim" in msg
+    rc, msg = _rc(lib, "amf_int4_sym_dense_attn", fake, 2, fake, fake, fake, fake, None, 0, 0, 0,
+                  0, fake, 2, 1, 8, 8, 1, 10, 128, 0.0, None, 0, None)
+    assert rc == wsp and "workspace" in msg
+    rc, msg = _rc(lib, "amf_int4_sym_dense_attn", fake, 2, fake + 2, fake, fake, fake, None, 0, 0,
+                  0, 0, fake, 2, 1, 8, 8, 1, 10, 128, 0.0, fake, 1 << 20, None)
+    assert rc == inv and "aligned" in msg
 
 
 @pytest.mark.skipif(not _no_device(), reason="argument-validation calls run on the CPU only")

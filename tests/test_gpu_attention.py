@@ -72,6 +72,141 @@ def test_dense_attention_mask_scale_and_edges():
     assert torch.count_nonzero(z).item() == 0
 
 
+def _dense_abi(q, k, v, mask, scale, workspace):
+    """amf_dense_attn through the C ABI with an explicit workspace (None:
+    the single-pass kernel), fp32 output."""
+    import amf_hip
+
+    B, Hq, Tq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    out = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+    mptr, ms = (0, (0, 0, 0, 0)) if mask is None else (mask.data_ptr(), mask.stride())
+    wptr = workspace.data_ptr() if workspace is not None else None
+    wsb = workspace.numel() if workspace is not None else 0
+    amf_hip.call("amf_dense_attn", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                 amf_hip.dtype_tag(q.dtype), mptr, *ms, out.data_ptr(), amf_hip.DTYPE_F32,
+                 B, Hq, Hkv, Tq, T, D, scale, wptr, wsb, amf_hip.stream_handle(DEV))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype,B,Hq,Hkv,Tq,T,D,masked", [
+    (torch.bfloat16, 1, 32, 8, 1, 20000, 128, False),  # few rows: many splits
+    (torch.float16, 2, 8, 1, 1, 4097, 64, True),        # GQA 8, ragged last chunk
+    (torch.float32, 1, 4, 2, 2, 3000, 256, True),
+    (torch.bfloat16, 3, 6, 3, 1, 65, 128, False),       # units not a multiple of 8
+])
+def test_dense_split_path_matches_f64_and_single_pass(dtype, B, Hq, Hkv, Tq, T, D, masked):
+    """The split (flash-decoding) path against float64 attention and the
+    single-pass kernel, with masks that empty whole splits and whole rows."""
+    import amf_hip
+
+    print(f"dense split case {dtype} B={B} Hq={Hq} Hkv={Hkv} Tq={Tq} T={T} D={D}", flush=True)
+    g = torch.Generator().manual_seed(T + D)
+    q = torch.randn(B, Hq, Tq, D, generator=g).to(dtype)
+    k = (torch.randn(B, Hkv, T, D, generator=g) * 2).to(dtype)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(dtype)
+    mask = None
+    if masked:
+        mask = torch.zeros(B, Hq, Tq, T)
+        mask[:, :, :, : T // 2] = float("-inf")   # the first half of the splits see nothing
+        mask[0, 1, 0, :] = float("-inf")          # one row sees nothing: NaN
+        mask[:, :, :, T - 7] = -2.5
+    ref = oatt.dense_attention_f64(_f64(q), _f64(k), _f64(v), 0.2,
+                                   None if mask is None else mask.numpy())
+    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Tq, T, D))
+    assert wsb > 0
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    dq, dk, dv = q.to(DEV), k.to(DEV), v.to(DEV)
+    dm = None if mask is None else mask.to(DEV)
+    split = _dense_abi(dq, dk, dv, dm, 0.2, ws)
+    single = _dense_abi(dq, dk, dv, dm, 0.2, None)
+    nan_ref = np.isnan(ref)
+    assert (np.isnan(split) == nan_ref).all() and (np.isnan(single) == nan_ref).all()
+    ok = ~nan_ref
+    assert float(np.abs(split[ok] - ref[ok]).max()) <= 1e-4
+    assert float(np.abs(split[ok] - single[ok]).max()) <= 1e-4
+    # a second call on the same workspace at a shorter context reuses it
+    T2 = T // 3 + 1
+    ref2 = oatt.dense_attention_f64(_f64(q), _f64(k[:, :, :T2]), _f64(v[:, :, :T2]), 0.2)
+    split2 = _dense_abi(dq, dk[:, :, :T2].contiguous(), dv[:, :, :T2].contiguous(), None, 0.2, ws)
+    assert float(np.abs(split2 - ref2).max()) <= 1e-4
+
+
+@pytest.mark.parametrize("dtype,lead,Hq,Hkv,Tq,T,D,masked", [
+    (torch.bfloat16, (4,), 32, 8, 1, 8192, 128, False),   # the positional decode workload
+    (torch.float16, (2,), 8, 1, 1, 1000, 64, True),
+    (torch.float32, (), 4, 2, 2, 300, 256, True),          # no lead dims: [H, T, D]
+    (torch.bfloat16, (2, 3), 4, 4, 1, 77, 128, False),     # two lead dims
+])
+def test_int4_sym_fused_matches_restore_path(dtype, lead, Hq, Hkv, Tq, T, D, masked):
+    """int4_sym CompressedKV K/V read in place (amf_int4_sym_dense_attn)
+    against the restore-then-attend path (decompress_to + amf_dense_attn) and
+    float64 attention over the restored values."""
+    from korith_vllm_ext.codecs import get_codec
+    from korith_vllm_ext.kernels import dense_attention, int4_sym_attention
+
+    print(f"int4_sym fused case {dtype} lead={lead} Hq={Hq} Hkv={Hkv} Tq={Tq} T={T} D={D}",
+          flush=True)
+    g = torch.Generator().manual_seed(T * 7 + D)
+    q = torch.randn(*lead, Hq, Tq, D, generator=g).to(dtype).to(DEV)
+    k = (torch.randn(*lead, Hkv, T, D, generator=g) * 2).to(dtype).to(DEV)
+    v = torch.randn(*lead, Hkv, T, D, generator=g).to(dtype).to(DEV)
+    codec = get_codec("int4_sym")
+    ck, cv = codec.compress(k), codec.compress(v)
+    mask = None
+    if masked:
+        mask = torch.zeros(Tq, T)
+        mask[:, : T // 3] = float("-inf")
+        mask[-1, T - 1] = -1.5
+        mask = mask.to(DEV)
+    fused = int4_sym_attention(q, ck, cv, 0.25, mask, torch.float32)
+    assert fused is not None
+    kd = codec.decompress_to(ck, dtype)
+    vd = codec.decompress_to(cv, dtype)
+    two = dense_attention(q, kd, vd, 0.25, mask, torch.float32)
+    torch.cuda.synchronize()
+    diff = float((fused - two).abs().max())
+    print(f"fused vs restore path: max |diff| {diff:.3e}", flush=True)
+    assert diff <= 1e-6
+    # the float64 oracle takes [batch, heads, tokens, head_dim]
+    ref = oatt.dense_attention_f64(_f64(q.reshape(-1, Hq, Tq, D)), _f64(kd.reshape(-1, Hkv, T, D)),
+                                   _f64(vd.reshape(-1, Hkv, T, D)), 0.25,
+                                   None if mask is None else mask.cpu().numpy())
+    assert float(np.abs(fused.reshape(-1, Hq, Tq, D).cpu().numpy() - ref).max()) <= 1e-4
+    # q's dtype out: the fp32 result rounded once
+    out = int4_sym_attention(q, ck, cv, 0.25, mask)
+    assert out.dtype == dtype and torch.equal(out, fused.to(dtype))
+
+
+def test_int4_sym_fused_empty_context_and_declines():
+    """kv_len 0 gives zeros, all -inf scores NaN; head dims outside
+    64/128/256 (32 here) and other formats decline (None), so the caller restores and
+    runs dense attention."""
+    import amf_hip
+    from korith_vllm_ext.codecs import get_codec
+    from korith_vllm_ext.kernels import int4_sym_attention
+
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(2, 4, 1, 128, generator=g).to(torch.bfloat16).to(DEV)
+    out = torch.full((2, 4, 1, 128), 7.0, device=DEV)
+    amf_hip.call("amf_int4_sym_dense_attn", q.data_ptr(), amf_hip.DTYPE_BF16, None, None, None,
+                 None, None, 0, 0, 0, 0, out.data_ptr(), amf_hip.DTYPE_F32, 2, 4, 4, 1, 0, 128,
+                 0.1, None, 0, amf_hip.stream_handle(DEV))
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out).item() == 0
+    codec = get_codec("int4_sym")
+    k0 = codec.compress(torch.randn(2, 4, 16, 128, generator=g).to(torch.bfloat16).to(DEV))
+    z = int4_sym_attention(q, k0, k0, None, torch.full((1, 16), float("-inf"), device=DEV))
+    assert z is not None and torch.isnan(z.float()).all()
+    q32 = torch.randn(2, 4, 1, 32, generator=g).to(torch.bfloat16).to(DEV)
+    k32 = codec.compress(torch.randn(2, 4, 16, 32, generator=g).to(torch.bfloat16).to(DEV))
+    assert int4_sym_attention(q32, k32, k32, None, None) is None
+    kf = get_codec("int4_sym_block").compress(
+        torch.randn(2, 4, 16, 128, generator=g).to(torch.bfloat16).to(DEV))
+    assert int4_sym_attention(q, kf, kf, None, None) is None
+
+
 def test_positional_contract_with_compressed_kv():
     """int4_decode_attention(q, CompressedKV, CompressedKV): K/V decompressed by
     the HIP codec, attention by the HIP kernel (dispatch.py:117-152 flow)."""
