@@ -653,10 +653,11 @@ class PositionalDecodeCase:
     """The reference's positional decode contract, int4_decode_attention(q, k,
     v) (int4_decode_attention.py:6-9 -> dispatch.py:117-143): K and V as
     int4_sym CompressedKV (per-channel INT4, the dispatch key) of [batch,
-    Hkv, tokens, D] bf16, q [batch, Hq, 1, D].  Here the call decompresses K
-    and V with the HIP codec and runs the HIP dense-attention kernel (GQA);
-    the reference materializes bf16 K/V the same way and then runs
-    matmul -> softmax -> matmul in bf16."""
+    Hkv, tokens, D] bf16, q [batch, Hq, 1, D].  The reference materializes
+    bf16 K/V and then runs matmul -> softmax -> matmul in bf16; here one
+    split-K kernel reads the codes in place and dequantizes each element to
+    the bf16 value the restore would write (amf_int4_sym_dense_attn), with a
+    merge launch after it."""
 
     def __init__(self, batch=4, tokens=8192, q_heads=32, kv_heads=8, head_dim=128, seed=21):
         from korith_vllm_ext.codecs import get_codec
@@ -709,8 +710,9 @@ class PositionalDecodeCase:
 
         def timed() -> dict:
             t, runs, total = cpu_time(run, min_runs, min_seconds)
-            k32 = oc.int4_channel_decompress(kd, ks, shape, torch.float32)[0].double().numpy()
-            v32 = oc.int4_channel_decompress(vd, vs, shape, torch.float32)[0].double().numpy()
+            # float64 attention over the restored bf16 K/V, the values both paths consume
+            k32 = oc.int4_channel_decompress(kd, ks, shape, torch.bfloat16)[0].double().numpy()
+            v32 = oc.int4_channel_decompress(vd, vs, shape, torch.bfloat16)[0].double().numpy()
             qq = q[0, :, 0].double().numpy()
             f64 = np.empty((self.Hq, self.D))
             for h in range(self.Hq):
@@ -1313,8 +1315,8 @@ def main() -> int:
             pd.algo_bytes, workload="positional_int4_sym_b4_8k", batch=pd.B, tokens=pd.T,
             q_heads=pd.Hq, kv_heads=pd.H,
             kv_tok_per_s=round(pd.B * pd.T / (tpd.median_ms * 1e-3), 1),
-            note="GB/s on the compressed K/V read; the call also writes and reads the "
-                 "decompressed bf16 K/V, as the reference's contract does")
+            note="GB/s on the compressed K/V read (codes + per-channel scales), the "
+                 "bytes the split-K kernel streams; the merge launch is in the time")
         log(f"positional decode: {result['positional_decode']}")
         if want_cpu:
             cpu_jobs.append(("positional_decode", "cpu_fallback", pd.cpu_fallback()))
