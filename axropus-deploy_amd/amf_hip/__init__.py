@@ -127,7 +127,7 @@ SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_i32, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i32,
          _c_i64, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_ptr, _c_i64, _c_ptr],
     ),
-    "amf_dense_attn_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i64, _c_i64, _c_i32]),
+    "amf_dense_attn_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32]),
     "amf_int4_sym_dense_attn": (
         _c_i32,
         [_c_ptr, _c_i32, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64,

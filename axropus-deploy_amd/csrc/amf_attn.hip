@@ -1,5 +1,6 @@
-// amf_attn.hip - dense scaled-dot-product attention over plain (already
-// dequantized) K/V rows: the positional path of int4_decode_attention.
+// amf_attn.hip - dense scaled-dot-product attention over plain K/V rows, or
+// over INT4_SYM codes dequantized in registers: the positional path of
+// int4_decode_attention.
 //
 // Computes out = softmax(q k^T * scale + mask) v for every query row, the
 // result of korith_vllm_ext/kernels/dispatch.py:117-143 (fallback_fp16_kernel,
@@ -10,15 +11,16 @@
 //
 // Split path (head_dim 64, 128 or 256, a caller workspace): flash decoding.
 // The KV tokens of a row are cut into splits sized so that the launch has
-// about kSplitWaves waves; one wave per (query row, split) streams its tokens
-// in 64-token chunks.  A K or V row is D / 8 lanes wide (16-byte loads, 8
-// elements per lane), so one wave load covers 64 / (D / 8) whole rows; the
-// score of a token is a reduction over its row's lanes, the online softmax
-// runs per lane on its rows' scores, and the PV product accumulates 8 dims
-// per lane.  Each split leaves (max, sum, acc[D]) in the workspace and a
-// merge kernel combines a row's splits with an LSE rescale.  The query rows
-// of one KV head are neighbouring waves, so their shared K/V rows are read
-// from HBM about once.
+// about kSplitWaves waves; one wave per (up to 4 query heads of a GQA group,
+// split) streams its tokens in batches of wave loads, each K/V row loaded
+// (and dequantized) once for all its heads.  A K or V row is D / 8 lanes
+// wide (16-byte loads, 8 elements per lane), so one wave load covers
+// 64 / (D / 8) whole rows; the score of a token is a reduction over its
+// row's lanes, the online softmax runs per lane on its rows' scores, and the
+// PV product accumulates 8 dims per lane and head.  Each split leaves (max,
+// sum, acc[D]) per head in the workspace and a merge kernel combines a row's
+// splits with an LSE rescale.  The waves of one KV head's group run on one
+// XCD, so what they share is read from HBM about once.
 //
 // Single-pass path (other head dims, kv_len 0, or no workspace): one
 // workgroup (4 waves) per query row.  Wave w takes the 64-token chunks w,
@@ -218,18 +220,33 @@ __global__ __launch_bounds__(kThreads) void dense_attn_kernel(AttnArgs a) {
 // ---------------------------------------------------------- split path --
 
 #ifndef AMF_DENSE_SPLIT_WAVES
-#define AMF_DENSE_SPLIT_WAVES 4096
+#define AMF_DENSE_SPLIT_WAVES 2048
+#endif
+#ifndef AMF_DENSE_MIN_CHUNKS
+#define AMF_DENSE_MIN_CHUNKS 1
 #endif
 constexpr int64_t kSplitWaves = AMF_DENSE_SPLIT_WAVES;  // waves one launch aims for
+constexpr int64_t kMinChunks = AMF_DENSE_MIN_CHUNKS;     // 64-token chunks per split, at least
 constexpr int kPartPad = 4;            // a split partial: acc[D], m, l, 2 pad (16-byte rows)
 constexpr int64_t kXcds = 8;           // XCDs of the chip, dealt workgroups round-robin
 
+// Query heads one wave of the split kernel serves: up to 4 of a GQA group
+// of G, so that it loads (and for INT4 dequantizes) each K/V row once for
+// all of them.
+inline int heads_per_wave(int32_t num_q_heads, int32_t num_kv_heads) {
+  const int G = num_q_heads / num_kv_heads;
+  return G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
+}
+
 // Splits per row and tokens per split (a multiple of 64) for `rows` query
-// rows over kv_len tokens: about kSplitWaves waves in all, at most one split
-// per 64-token chunk.
-inline void dense_splits(int64_t rows, int64_t kv_len, int64_t* n_splits, int64_t* split_tokens) {
+// rows, hpw of them per wave, over kv_len tokens: about kSplitWaves waves
+// in all, at least kMinChunks and at most all 64-token chunks per split.
+inline void dense_splits(int64_t rows, int hpw, int64_t kv_len, int64_t* n_splits,
+                         int64_t* split_tokens) {
   const int64_t chunks = (kv_len + 63) / 64;
-  int64_t n = (kSplitWaves + rows - 1) / rows;
+  const int64_t wave_rows = rows / hpw;
+  int64_t n = (kSplitWaves + wave_rows - 1) / wave_rows;
+  n = std::min<int64_t>(n, (chunks + kMinChunks - 1) / kMinChunks);
   n = std::max<int64_t>(1, std::min<int64_t>(n, chunks));
   const int64_t per = (chunks + n - 1) / n;  // chunks per split
   *split_tokens = per * 64;
@@ -343,39 +360,52 @@ struct RawRow<DT, true> {
   }
 };
 
-// Wave loads one batch keeps in flight per operand.
-template <int DT, bool INT4>
-constexpr int kBatchLoads = (!INT4 && DT == AMF_DTYPE_F32) ? 8 : 16;
+#ifndef AMF_DENSE_BATCH
+#define AMF_DENSE_BATCH 8
+#endif
 
-template <int DT, int LPR, bool INT4>
+// One wave per (query rows of GH heads of a GQA group, split).  LPR =
+// head_dim / 8 lanes per K/V row, TPS = 64 / LPR rows per wave load; lane
+// (g = lane / LPR, c = lane % LPR) holds elements 8c .. 8c + 7 of the GH
+// query rows and, in step i of a batch, of K/V row t0 + TPS i + g, which it
+// loads (and for INT4 dequantizes) once for all GH heads.
+template <int DT, int LPR, bool INT4, int GH>
 __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float* part,
                                                               int64_t split_tokens,
                                                               int64_t n_splits, int64_t units) {
   constexpr int TPS = 64 / LPR;
-  constexpr int STEPS = LPR;  // 64-token chunk = STEPS loads of TPS rows
+  // Steps of a batch: its K (and, for INT4, V) loads are all issued before
+  // the first is used.
+  constexpr int SB = LPR < AMF_DENSE_BATCH ? LPR : AMF_DENSE_BATCH;
+  constexpr int BT = TPS * SB;  // tokens per batch, divides 64
+  using Raw = RawRow<DT, INT4>;
   const int lane = threadIdx.x, g = lane / LPR, c = lane % LPR;
   const int G = a.num_q_heads / a.num_kv_heads;
+  const int W = G / GH;  // waves per unit
   const int64_t id = blockIdx.x, slot = id / kXcds;
-  const int r = (int)(slot % G);
-  const int64_t u = (slot / G) * kXcds + id % kXcds;
+  const int r = (int)(slot % W);
+  const int64_t u = (slot / W) * kXcds + id % kXcds;
   if (u >= units) return;
   const int64_t split = u % n_splits, rest = u / n_splits;
   const int64_t tq = rest % a.q_len, bkv = rest / a.q_len;
   const int hkv = (int)(bkv % a.num_kv_heads);
   const int64_t b = bkv / a.num_kv_heads;
-  const int h = hkv * G + r;
-  const int64_t row = (b * a.num_q_heads + h) * a.q_len + tq;  // (b, h, tq) flattened
+  const int h0 = hkv * G + r * GH;  // first of this wave's query heads
   const int D = 8 * LPR;
   const int64_t T = a.kv_len;
   const int64_t t_begin = split * split_tokens, t_end = min(T, t_begin + split_tokens);
   const int64_t kv_base = (b * a.num_kv_heads + hkv) * T;
-  const float* mrow = a.mask ? a.mask + b * a.ms0 + (int64_t)h * a.ms1 + tq * a.ms2 : nullptr;
   const float qs = a.scale * kLog2e;
+  // query row of head h0 + j: (b, h0 + j, tq) flattened
+  auto qrow = [&](int j) { return (b * a.num_q_heads + h0 + j) * a.q_len + tq; };
 
-  float q[8];
-  elem8<DT>(a.q, row * D + 8 * c, q);
+  float q[GH][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) q[e] *= qs;
+  for (int j = 0; j < GH; ++j) {
+    elem8<DT>(a.q, qrow(j) * D + 8 * c, q[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[j][e] *= qs;
+  }
   float ksc[8], vsc[8];  // this lane's 8 channels' scales (INT4)
   if constexpr (INT4) {
 #pragma unroll
@@ -384,16 +414,16 @@ __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float*
       vsc[e] = (float)a.v_scales[8 * c + e];
     }
   }
-  float m_run = -INFINITY, l_run = 0.0f;  // l_run: this lane's group's tokens
-  float acc[8];
+  float m_run[GH], l_run[GH];  // l_run: this lane's row group's tokens
+  float acc[GH][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int j = 0; j < GH; ++j) {
+    m_run[j] = -INFINITY;
+    l_run[j] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
+  }
 
-  // A batch is SB wave loads of TPS rows each; its K (and, for INT4, V)
-  // loads are all issued before the first is used.
-  constexpr int SB = STEPS < kBatchLoads<DT, INT4> ? STEPS : kBatchLoads<DT, INT4>;
-  constexpr int BT = TPS * SB;  // tokens per batch, divides 64
-  using Raw = RawRow<DT, INT4>;
   for (int64_t t0 = t_begin; t0 < t_end; t0 += BT) {
     Raw kr[SB];
     Raw vr[INT4 ? SB : 1];
@@ -409,78 +439,96 @@ __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float*
         vr[i] = Raw::load(a.v, kv_base + (t < t_end ? t : t_begin), c, D);
       }
     }
-    float mk[SB];
-    if (mrow) {
-#pragma unroll
-      for (int i = 0; i < SB; ++i) {
-        const int64_t t = t0 + TPS * i + g;
-        mk[i] = mrow[(t < t_end ? t : t_begin) * a.ms3];
-      }
-    }
-    float sc[SB];
+    float sc[GH][SB];
 #pragma unroll
     for (int i = 0; i < SB; ++i) {
       float x[8];
       kr[i].decode(ksc, x);
-      float d = q[0] * x[0];
 #pragma unroll
-      for (int e = 1; e < 8; ++e) d = fmaf(q[e], x[e], d);
-      d = group_sum<LPR>(d);
-      if (mrow) d = fmaf(mk[i], kLog2e, d);
-      sc[i] = t0 + TPS * i + g < t_end ? d : -INFINITY;
+      for (int j = 0; j < GH; ++j) {
+        float d = q[j][0] * x[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) d = fmaf(q[j][e], x[e], d);
+        sc[j][i] = group_sum<LPR>(d);
+      }
     }
-    float mc = sc[0];
+    if (a.mask) {  // additive mask, per head
 #pragma unroll
-    for (int i = 1; i < SB; ++i) mc = fmaxf(mc, sc[i]);
-    mc = across_groups_max<LPR>(mc);
-    const float m_new = fmaxf(m_run, mc);
-    if (m_new == -INFINITY) continue;  // every score so far is -inf (wave-uniform)
-    const float alpha = exp2f(m_run - m_new);
-    l_run *= alpha;
+      for (int j = 0; j < GH; ++j) {
+        const float* mrow = a.mask + b * a.ms0 + (int64_t)(h0 + j) * a.ms1 + tq * a.ms2;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+        for (int i = 0; i < SB; ++i) {
+          const int64_t t = t0 + TPS * i + g;
+          sc[j][i] = fmaf(mrow[(t < t_end ? t : t_begin) * a.ms3], kLog2e, sc[j][i]);
+        }
+      }
+    }
+    float m_new[GH];
+    bool live = false;
+#pragma unroll
+    for (int j = 0; j < GH; ++j) {
+#pragma unroll
+      for (int i = 0; i < SB; ++i)
+        if (t0 + TPS * i + g >= t_end) sc[j][i] = -INFINITY;
+      float mc = sc[j][0];
+#pragma unroll
+      for (int i = 1; i < SB; ++i) mc = fmaxf(mc, sc[j][i]);
+      mc = across_groups_max<LPR>(mc);
+      m_new[j] = fmaxf(m_run[j], mc);
+      live = live || m_new[j] != -INFINITY;
+    }
+    if (!live) continue;  // every score so far is -inf for every head (wave-uniform)
+#pragma unroll
+    for (int j = 0; j < GH; ++j) {
+      // a head with every score so far -inf keeps l = 0, acc = 0
+      const float alpha = m_new[j] == -INFINITY ? 1.0f : exp2f(m_run[j] - m_new[j]);
+      l_run[j] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[j][e] *= alpha;
+    }
+    Raw vd[INT4 ? 1 : SB];
     if constexpr (!INT4) {
       // dense V: loaded after the scores, all SB loads in flight together
-      Raw vd[SB];
 #pragma unroll
       for (int i = 0; i < SB; ++i) {
         const int64_t t = t0 + TPS * i + g;
         vd[i] = Raw::load(a.v, kv_base + (t < t_end ? t : t_begin), c, D);
       }
+    }
 #pragma unroll
-      for (int i = 0; i < SB; ++i) {
-        const float p = sc[i] == -INFINITY ? 0.0f : exp2f(sc[i] - m_new);
-        l_run += p;
-        float x[8];
+    for (int i = 0; i < SB; ++i) {
+      float x[8];
+      if constexpr (INT4)
+        vr[i].decode(vsc, x);
+      else
         vd[i].decode(vsc, x);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, x[e], acc[e]);
-      }
-    } else {
+      for (int j = 0; j < GH; ++j) {
+        const float p = sc[j][i] == -INFINITY ? 0.0f : exp2f(sc[j][i] - m_new[j]);
+        l_run[j] += p;
 #pragma unroll
-      for (int i = 0; i < SB; ++i) {
-        const float p = sc[i] == -INFINITY ? 0.0f : exp2f(sc[i] - m_new);
-        l_run += p;
-        float x[8];
-        vr[i].decode(vsc, x);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, x[e], acc[e]);
+        for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(p, x[e], acc[j][e]);
       }
     }
-    m_run = m_new;
+#pragma unroll
+    for (int j = 0; j < GH; ++j) m_run[j] = m_new[j];
   }
   // the row groups hold disjoint tokens: add them up
-  l_run = across_groups_sum<LPR>(l_run);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = across_groups_sum<LPR>(acc[e]);
-  float* pr = part + (row * n_splits + split) * (int64_t)(D + kPartPad);
-  if (g == 0) {
-    *reinterpret_cast<f32x4*>(pr + 8 * c) = f32x4{acc[0], acc[1], acc[2], acc[3]};
-    *reinterpret_cast<f32x4*>(pr + 8 * c + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
-  }
-  if (lane == 0) {
-    pr[D] = m_run;
-    pr[D + 1] = l_run;
+  for (int j = 0; j < GH; ++j) {
+    const float l = across_groups_sum<LPR>(l_run[j]);
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = across_groups_sum<LPR>(acc[j][e]);
+    float* pr = part + (qrow(j) * n_splits + split) * (int64_t)(D + kPartPad);
+    if (g == 0) {
+      *reinterpret_cast<f32x4*>(pr + 8 * c) = f32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<f32x4*>(pr + 8 * c + 4) = f32x4{o[4], o[5], o[6], o[7]};
+    }
+    if (lane == 0) {
+      pr[D] = m_run[j];
+      pr[D + 1] = l;
+    }
   }
 }
 
@@ -545,12 +593,27 @@ __global__ __launch_bounds__(64) void dense_attn_merge_kernel(AttnArgs a, const 
   }
 }
 
-// Workgroups of the split launch: units rounded up to the XCD count, times G.
+// Workgroups of the split launch: units (b, KV head, query row, split)
+// rounded up to the XCD count, times the waves per unit.
 inline int64_t split_grid(int64_t rows, int64_t n_splits, int32_t num_q_heads,
                           int32_t num_kv_heads, int64_t* units) {
   const int64_t G = num_q_heads / num_kv_heads;
   *units = rows / G * n_splits;
-  return (*units + kXcds - 1) / kXcds * kXcds * G;
+  return (*units + kXcds - 1) / kXcds * kXcds * (G / heads_per_wave(num_q_heads, num_kv_heads));
+}
+
+template <int DT, bool INT4, int GH>
+void launch_split_gh(const AttnArgs& a, float* part, int64_t split_tokens, int64_t n_splits,
+                     dim3 grid, int64_t units, hipStream_t st) {
+  if (a.head_dim == 64)
+    dense_attn_split_kernel<DT, 8, INT4, GH>
+        <<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits, units);
+  else if (a.head_dim == 128)
+    dense_attn_split_kernel<DT, 16, INT4, GH>
+        <<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits, units);
+  else
+    dense_attn_split_kernel<DT, 32, INT4, GH>
+        <<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits, units);
 }
 
 template <int DT, bool INT4>
@@ -558,15 +621,13 @@ void launch_split(const AttnArgs& a, int32_t out_dtype, int64_t rows, float* par
                   int64_t split_tokens, int64_t n_splits, hipStream_t st) {
   int64_t units = 0;
   const dim3 grid((unsigned)split_grid(rows, n_splits, a.num_q_heads, a.num_kv_heads, &units));
-  if (a.head_dim == 64)
-    dense_attn_split_kernel<DT, 8, INT4><<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits,
-                                                               units);
-  else if (a.head_dim == 128)
-    dense_attn_split_kernel<DT, 16, INT4><<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits,
-                                                                units);
+  const int gh = heads_per_wave(a.num_q_heads, a.num_kv_heads);
+  if (gh == 4)
+    launch_split_gh<DT, INT4, 4>(a, part, split_tokens, n_splits, grid, units, st);
+  else if (gh == 2)
+    launch_split_gh<DT, INT4, 2>(a, part, split_tokens, n_splits, grid, units, st);
   else
-    dense_attn_split_kernel<DT, 32, INT4><<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits,
-                                                                units);
+    launch_split_gh<DT, INT4, 1>(a, part, split_tokens, n_splits, grid, units, st);
   const dim3 mgrid((unsigned)rows);
 #define AMF_MERGE(OUT)                                                                   \
   if (a.head_dim == 64)                                                                  \
@@ -633,15 +694,16 @@ int check_attn_args(const char* who, int32_t dtype, int32_t out_dtype, int64_t b
 }  // namespace
 
 extern "C" int64_t amf_dense_attn_workspace_bytes(int64_t batch, int32_t num_q_heads,
-                                                  int64_t q_len, int64_t kv_len,
-                                                  int32_t head_dim) {
-  if (batch <= 0 || num_q_heads <= 0 || q_len <= 0 || kv_len <= 0 || !split_head_dim(head_dim) ||
-      batch > 0x7FFFFFFF || q_len > 0x7FFFFFFF)
+                                                  int32_t num_kv_heads, int64_t q_len,
+                                                  int64_t kv_len, int32_t head_dim) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+      q_len <= 0 || kv_len <= 0 || !split_head_dim(head_dim) || batch > 0x7FFFFFFF ||
+      q_len > 0x7FFFFFFF)
     return 0;
   const int64_t rows = batch * num_q_heads * q_len;
   if (rows > 0x7FFFFFFF) return 0;
   int64_t n_splits = 1, split_tokens = 64;
-  dense_splits(rows, kv_len, &n_splits, &split_tokens);
+  dense_splits(rows, heads_per_wave(num_q_heads, num_kv_heads), kv_len, &n_splits, &split_tokens);
   // The split launch has at most rows * n_splits + 8 * num_q_heads
   // workgroups; a shape beyond one launch takes the single-pass kernel.
   if (rows > (0x7FFFFFFF - kXcds * num_q_heads) / n_splits) return 0;
@@ -672,11 +734,12 @@ extern "C" int amf_dense_attn(const void* q, const void* k, const void* v, int32
              softmax_scale, nullptr, nullptr};
   hipStream_t st = as_stream(stream);
   const int64_t need =
-      amf_dense_attn_workspace_bytes(batch, num_q_heads, q_len, kv_len, head_dim);
+      amf_dense_attn_workspace_bytes(batch, num_q_heads, num_kv_heads, q_len, kv_len, head_dim);
   if (need > 0 && vec8 && ((uintptr_t)q % 16) == 0 && workspace && workspace_bytes >= need &&
       ((uintptr_t)workspace % 16) == 0) {
     int64_t n_splits = 1, split_tokens = 64;
-    dense_splits(rows, kv_len, &n_splits, &split_tokens);
+    dense_splits(rows, heads_per_wave(num_q_heads, num_kv_heads), kv_len, &n_splits,
+                 &split_tokens);
     float* part = static_cast<float*>(workspace);
     if (dtype == AMF_DTYPE_F32)
       launch_split<AMF_DTYPE_F32, false>(a, out_dtype, rows, part, split_tokens, n_splits, st);
@@ -733,7 +796,7 @@ extern "C" int amf_int4_sym_dense_attn(const void* q, int32_t dtype, const void*
     return check_launch(who);
   }
   const int64_t need =
-      amf_dense_attn_workspace_bytes(batch, num_q_heads, q_len, kv_len, head_dim);
+      amf_dense_attn_workspace_bytes(batch, num_q_heads, num_kv_heads, q_len, kv_len, head_dim);
   if (need == 0)
     return fail(AMF_ERR_UNSUPPORTED, "%s: %lld query rows exceed one launch", who,
                 (long long)rows);
@@ -741,7 +804,8 @@ extern "C" int amf_int4_sym_dense_attn(const void* q, int32_t dtype, const void*
     return fail(AMF_ERR_WORKSPACE, "%s: needs %lld workspace bytes (16-byte aligned)", who,
                 (long long)need);
   int64_t n_splits = 1, split_tokens = 64;
-  dense_splits(rows, kv_len, &n_splits, &split_tokens);
+  dense_splits(rows, heads_per_wave(num_q_heads, num_kv_heads), kv_len, &n_splits,
+               &split_tokens);
   float* part = static_cast<float*>(workspace);
   if (dtype == AMF_DTYPE_F32)
     launch_split<AMF_DTYPE_F32, true>(a, out_dtype, rows, part, split_tokens, n_splits, st);

@@ -150,7 +150,7 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Op
         mptr, ms = m4.data_ptr(), tuple(m4.stride())
     # split-K scratch (per-split softmax partials), 0 bytes when the shape
     # takes the single-pass kernel
-    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Tq, T, D))
+    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Hkv, Tq, T, D))
     ws = torch.empty(wsb, dtype=torch.uint8, device=q.device) if wsb else None
     amf_hip.call("amf_dense_attn", qc.data_ptr(), k.data_ptr(), v.data_ptr(),
                  amf_hip.dtype_tag(q.dtype), mptr, ms[0], ms[1], ms[2], ms[3], out.data_ptr(),
@@ -216,7 +216,7 @@ def int4_sym_attention(q: torch.Tensor, k: Any, v: Any, scale: Optional[float],
         m4 = mask.to(device=q.device, dtype=torch.float32).expand(*q.shape[:-3], Hq, Tq, T)
         m4 = m4.reshape(B, Hq, Tq, T)
         mptr, ms = m4.data_ptr(), tuple(m4.stride())
-    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Tq, T, D))
+    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Hkv, Tq, T, D))
     if T > 0 and wsb == 0:
         return None  # beyond one split launch: the restoring path takes it
     ws = torch.empty(wsb, dtype=torch.uint8, device=q.device) if wsb else None

@@ -362,7 +362,8 @@ int amf_dense_attn(const void* q, const void* k, const void* v, int32_t dtype,
 
 /* Workspace bytes amf_dense_attn needs for its split path at this shape; 0
  * when the shape takes the single-pass path (then pass NULL, 0). */
-int64_t amf_dense_attn_workspace_bytes(int64_t batch, int32_t num_q_heads, int64_t q_len,
+int64_t amf_dense_attn_workspace_bytes(int64_t batch, int32_t num_q_heads,
+                                       int32_t num_kv_heads, int64_t q_len,
                                        int64_t kv_len, int32_t head_dim);
 
 /* amf_dense_attn over INT4_SYM K and V without materialising them: k_codes

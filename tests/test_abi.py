@@ -102,15 +102,21 @@ def _no_device():
 
 def test_dense_attn_workspace_bytes(lib):
     """Host-only size query: split partials of (head_dim + 4) fp32 per
-    (query row, split), splits aiming at 4096 waves, one per 64-token chunk
-    at most; 0 where the single-pass kernel runs."""
+    (query row, split); a wave serves up to 4 query heads of a GQA group and
+    the splits aim at 2048 waves, one 64-token chunk per split at least; 0
+    where the single-pass kernel runs."""
     f = lib.amf_dense_attn_workspace_bytes
-    assert f(4, 32, 1, 8192, 128) == 128 * 32 * (128 + 4) * 4   # 32 splits of 256 tokens
-    assert f(1, 32, 1, 20000, 128) == 32 * 105 * 132 * 4        # 105 splits of 192 tokens
-    assert f(1, 2, 1, 1, 256) == 2 * 1 * 260 * 4
-    assert f(64, 64, 1, 100, 64) == 4096 * 1 * 68 * 4            # rows fill the launch alone
-    assert f(4, 32, 1, 8192, 80) == 0 and f(4, 32, 1, 0, 128) == 0
-    assert f(0, 32, 1, 8192, 128) == 0 and f(1 << 40, 32, 1, 64, 128) == 0
+    # 128 rows, 4 per wave -> 32 wave rows -> 64 splits of 128 tokens
+    assert f(4, 32, 8, 1, 8192, 128) == 128 * 64 * (128 + 4) * 4
+    # 32 rows -> 8 wave rows -> 256 splits wanted, 313 chunks -> 157 splits of 128 tokens
+    assert f(1, 32, 8, 1, 20000, 128) == 32 * 157 * 132 * 4
+    assert f(1, 2, 2, 1, 1, 256) == 2 * 1 * 260 * 4
+    # GQA 3: one head per wave; 24 wave rows -> 86 splits wanted, 79 chunks -> 79 splits
+    assert f(2, 12, 4, 1, 5000, 64) == 24 * 79 * 68 * 4
+    assert f(64, 64, 8, 1, 100, 64) == 4096 * 2 * 68 * 4
+    assert f(4, 32, 8, 1, 8192, 80) == 0 and f(4, 32, 8, 1, 0, 128) == 0
+    assert f(0, 32, 8, 1, 8192, 128) == 0 and f(1 << 40, 32, 8, 1, 64, 128) == 0
+    assert f(4, 32, 7, 1, 8192, 128) == 0  # heads not a multiple: no split path
 
 
 # Fake addresses below are never dereferenced because every call fails

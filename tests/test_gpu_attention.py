@@ -95,6 +95,8 @@ def _dense_abi(q, k, v, mask, scale, workspace):
     (torch.float16, 2, 8, 1, 1, 4097, 64, True),        # GQA 8, ragged last chunk
     (torch.float32, 1, 4, 2, 2, 3000, 256, True),
     (torch.bfloat16, 3, 6, 3, 1, 65, 128, False),       # units not a multiple of 8
+    (torch.bfloat16, 2, 6, 1, 1, 700, 64, False),       # GQA 6: 3 waves of 2 heads
+    (torch.float16, 1, 12, 4, 2, 333, 128, True),       # GQA 3: one head per wave
 ])
 def test_dense_split_path_matches_f64_and_single_pass(dtype, B, Hq, Hkv, Tq, T, D, masked):
     """The split (flash-decoding) path against float64 attention and the
@@ -114,7 +116,7 @@ def test_dense_split_path_matches_f64_and_single_pass(dtype, B, Hq, Hkv, Tq, T, 
         mask[:, :, :, T - 7] = -2.5
     ref = oatt.dense_attention_f64(_f64(q), _f64(k), _f64(v), 0.2,
                                    None if mask is None else mask.numpy())
-    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Tq, T, D))
+    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Hkv, Tq, T, D))
     assert wsb > 0
     ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
     dq, dk, dv = q.to(DEV), k.to(DEV), v.to(DEV)
