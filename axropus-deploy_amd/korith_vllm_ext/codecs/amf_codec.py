@@ -169,6 +169,26 @@ class _HipCodec(Codec):
             return 16
         return max(T, 1)
 
+    def _flat_rows(self, x: torch.Tensor) -> int:
+        """Rows per page when x is compressed as one plane of its D-element
+        rows, else 0.  The per-tensor FP8 scale and the per-channel INT4
+        scales do not depend on paging, and the codes keep the input's
+        memory order either way, so a tensor whose dim -3 is short (e.g.
+        [batch, kv_heads, tokens, head_dim]) is cut into pages of about 16K
+        elements instead of a few pages of dim -3's length.  The rows per
+        page are the largest power of two up to 16384 / D dividing the row
+        count, and a page must fill one workgroup pass (2048 elements)."""
+        if self.FORMAT not in (FMT_FP8_E4M3, FMT_INT4_SYM) or self._is_page_tensor(x):
+            return 0
+        D = int(x.shape[-1])
+        if D <= 0 or x.numel() == 0:
+            return 0
+        rows = x.numel() // D
+        bs = 1
+        while bs * 2 * D <= 16384 and rows % (bs * 2) == 0:
+            bs *= 2
+        return bs if bs * D >= 2048 else 0
+
     def _is_page_tensor(self, x: torch.Tensor) -> bool:
         """A layer page tensor [2, nb, bs, H, D] whose pages are exactly the
         dense grouping of [..., T=bs, H, D]: compressed as 2 planes of nb
@@ -185,10 +205,18 @@ class _HipCodec(Codec):
     def compress(self, raw_kv: torch.Tensor) -> CompressedKV:
         self._check_input(raw_kv)
         x = raw_kv.detach().contiguous()
+        flat = self._flat_rows(x)
         if self._is_page_tensor(x):
             _, nb, bs, H, D = x.shape
             view = _paged.planes_view([x[0], x[1]])
             n_pages, page, T = nb, bs, nb * bs
+        elif flat:
+            # one plane of D-element rows in memory order, `flat` rows a page
+            D, H = int(x.shape[-1]), 1
+            T = x.numel() // D
+            page, n_pages = flat, T // flat
+            view = _paged.CacheView([x.data_ptr()], page * D * x.element_size(), n_pages, page,
+                                    1, D, x.dtype, x.device, keep=[x])
         else:
             T, H, D = x.shape[-3:]
             page = self._page_tokens(T)

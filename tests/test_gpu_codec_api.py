@@ -41,15 +41,24 @@ def test_roundtrip_shape_dtype_error_ratio(fmt, sample_kv):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(2, 256, 8, 128), (300, 4, 64), (3, 2, 40, 2, 64)])
+@pytest.mark.parametrize("shape", [(2, 256, 8, 128), (300, 4, 64), (3, 2, 40, 2, 64),
+                                   (2, 8, 1024, 128), (3, 5, 7, 64)])
 def test_reference_formats_bitexact(dtype, shape):
+    """Codes, scales and restored values of the reference formats against the
+    oracle.  Shapes whose row count has a power-of-two factor of at least
+    2048 / head_dim are compressed as pages of rows ((2, 256, 8, 128),
+    (3, 2, 40, 2, 64) and the [batch, kv_heads, tokens, head_dim] tensor
+    (2, 8, 1024, 128)); the others as pages of dim -3."""
     from korith_vllm_ext.codecs import get_codec
 
     g = torch.Generator().manual_seed(sum(shape))
     x = (torch.randn(*shape, generator=g) * 3).to(dtype)
     dx = x.to(DEV)
+    rows = x.numel() // shape[-1]
+    flat = any(rows % b == 0 and b * shape[-1] >= 2048 for b in (16, 32, 64, 128, 256))
     # fp8_e4m3: codes, the Python-double tensor_scale and the decompression
     c = get_codec("fp8_e4m3").compress(dx)
+    assert (c.meta["_layout"].num_heads == 1 and c.meta["_layout"].n_planes == 1) == flat
     codes, scale = oc.fp8_tensor_compress(x)
     assert c.data.dtype == torch.float8_e4m3fn and c.data.shape == x.shape
     assert torch.equal(c.data.view(torch.uint8).cpu(), codes)
@@ -60,6 +69,7 @@ def test_reference_formats_bitexact(dtype, shape):
         assert torch.equal(got, oc.fp8_tensor_decompress(codes, scale, tdt))
     # int4_sym: packed codes, fp16 channel scales, decompression
     c = get_codec("int4_sym").compress(dx)
+    assert (c.meta["_layout"].num_heads == 1 and c.meta["_layout"].n_planes == 1) == flat
     packed, sc = oc.int4_channel_compress(x)
     assert torch.equal(c.data.cpu(), packed) and torch.equal(c.scales.cpu(), sc)
     got = get_codec("int4_sym").decompress_to(c, torch.float32).cpu()
