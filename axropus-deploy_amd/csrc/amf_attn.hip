@@ -40,6 +40,8 @@ namespace {
 
 using amf::u32x4;
 using amf::f32x4;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
@@ -302,25 +304,53 @@ __device__ __forceinline__ float across_groups_max(float x) {
 // INT4 = true: K and V are INT4_SYM codes, dequantized as the codec's restore
 // does, (code - 8) * scale in fp32 rounded to DT (the dtype the restore would
 // write and q's dtype), so the scores see the values a decompressed tensor
-// holds.
+// holds.  (code - 8) * s is taken as fma(code, s, -8 s): the exact product
+// fits fp32 (4 + 11 bits), so the single rounding of the fma is exact too.
+// The nibbles go to bytes first (even elements in w & 0x0F0F0F0F, odd ones
+// in (w >> 4) & 0x0F0F0F0F), so that v_cvt_f32_ubyte0..3 convert them; the
+// empty asm keeps the compiler from folding that back into a bit-field
+// extract per element.
 template <int DT>
-__device__ __forceinline__ void int4_sym_row8(uint32_t w, const float (&s)[8], float (&x)[8]) {
-#pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    float y = ((float)__builtin_amdgcn_ubfe(w, 4 * n, 4) - 8.0f) * s[n];
-    if constexpr (DT == AMF_DTYPE_BF16) {
-      y = (float)(__bf16)y;
-    } else if constexpr (DT == AMF_DTYPE_F16) {
-      amf::keep_f32(y);
-      y = (float)(_Float16)y;
-    }
-    x[n] = y;
+__device__ __forceinline__ float round_to(float y) {
+  if constexpr (DT == AMF_DTYPE_BF16) {
+    return (float)(__bf16)y;
+  } else if constexpr (DT == AMF_DTYPE_F16) {
+    amf::keep_f32(y);
+    return (float)(_Float16)y;
+  } else {
+    return y;
   }
+}
+
+// The 8 exact products (code - 8) * scale of one code word, before rounding.
+__device__ __forceinline__ void int4_sym_vals(uint32_t w, const float (&s)[8], const float (&z)[8],
+                                              float (&y)[8]) {
+  uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;
+  asm("" : "+v"(ev));
+  asm("" : "+v"(od));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    y[2 * i] = __builtin_fmaf((float)((ev >> (8 * i)) & 0xFFu), s[2 * i], z[2 * i]);
+    y[2 * i + 1] = __builtin_fmaf((float)((od >> (8 * i)) & 0xFFu), s[2 * i + 1], z[2 * i + 1]);
+  }
+}
+
+// a.lo * b.lo + a.hi * b.hi + c for two bf16 or fp16 pairs (fp32 products
+// and sum).
+template <int DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT == AMF_DTYPE_BF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
+                                  c, false);
 }
 
 // One lane's 8 elements of a K/V row as loaded (lane c of a row group holds
 // dims 8c .. 8c + 7 of a head_dim-D row): a code word for INT4, else 16
-// (bf16/fp16) or 32 (fp32) bytes.
+// (bf16/fp16) or 32 (fp32) bytes.  decode() gives them as fp32; pairs()
+// (bf16/fp16 only) as four DT pairs, elements 2i and 2i + 1 in word i.
 template <int DT, bool INT4>
 struct RawRow {  // bf16 / fp16
   u32x4 w;
@@ -328,8 +358,16 @@ struct RawRow {  // bf16 / fp16
     return RawRow{*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + r * D +
                                                   8 * c)};
   }
-  __device__ __forceinline__ void decode(const float (&)[8], float (&x)[8]) const {
+  __device__ __forceinline__ void decode(const float (&)[8], const float (&)[8],
+                                         float (&x)[8]) const {
     amf::unpack8<DT == AMF_DTYPE_BF16>(w, x);
+  }
+  __device__ __forceinline__ void pairs(const float (&)[8], const float (&)[8],
+                                        uint32_t (&pr)[4]) const {
+    pr[0] = w.x;
+    pr[1] = w.y;
+    pr[2] = w.z;
+    pr[3] = w.w;
   }
 };
 
@@ -340,7 +378,8 @@ struct RawRow<AMF_DTYPE_F32, false> {
     const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + r * D + 8 * c);
     return RawRow{p[0], p[1]};
   }
-  __device__ __forceinline__ void decode(const float (&)[8], float (&x)[8]) const {
+  __device__ __forceinline__ void decode(const float (&)[8], const float (&)[8],
+                                         float (&x)[8]) const {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       x[e] = lo[e];
@@ -355,8 +394,20 @@ struct RawRow<DT, true> {
   static __device__ __forceinline__ RawRow load(const void* base, int64_t r, int c, int D) {
     return RawRow{static_cast<const uint32_t*>(base)[r * (D / 8) + c]};
   }
-  __device__ __forceinline__ void decode(const float (&s)[8], float (&x)[8]) const {
-    int4_sym_row8<DT>(w, s, x);
+  __device__ __forceinline__ void decode(const float (&s)[8], const float (&z)[8],
+                                         float (&x)[8]) const {
+    float y[8];
+    int4_sym_vals(w, s, z, y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = round_to<DT>(y[e]);
+  }
+  __device__ __forceinline__ void pairs(const float (&s)[8], const float (&z)[8],
+                                        uint32_t (&pr)[4]) const {
+    float y[8];
+    int4_sym_vals(w, s, z, y);
+    // round to nearest even, as decode() and the restore do
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = amf::pack2<DT == AMF_DTYPE_BF16>(y[2 * i], y[2 * i + 1]);
   }
 };
 
@@ -399,19 +450,35 @@ __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float*
   // query row of head h0 + j: (b, h0 + j, tq) flattened
   auto qrow = [&](int j) { return (b * a.num_q_heads + h0 + j) * a.q_len + tq; };
 
-  float q[GH][8];
+  // bf16 / fp16: scores are v_dot2 products of K pairs and the query's own
+  // pairs, scaled afterwards; fp32: fma chains on the pre-scaled query.
+  constexpr bool PK = DT != AMF_DTYPE_F32;
+  float q[PK ? 1 : GH][8];
+  uint32_t qp[PK ? GH : 1][4];
 #pragma unroll
   for (int j = 0; j < GH; ++j) {
-    elem8<DT>(a.q, qrow(j) * D + 8 * c, q[j]);
+    if constexpr (PK) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) +
+                                                      qrow(j) * D + 8 * c);
+      qp[j][0] = v.x;
+      qp[j][1] = v.y;
+      qp[j][2] = v.z;
+      qp[j][3] = v.w;
+    } else {
+      elem8<DT>(a.q, qrow(j) * D + 8 * c, q[j]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) q[j][e] *= qs;
+      for (int e = 0; e < 8; ++e) q[j][e] *= qs;
+    }
   }
-  float ksc[8], vsc[8];  // this lane's 8 channels' scales (INT4)
+  // this lane's 8 channels' scales s and -8 s (INT4)
+  float ksc[8], kz[8], vsc[8], vz[8];
   if constexpr (INT4) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       ksc[e] = (float)a.k_scales[8 * c + e];
       vsc[e] = (float)a.v_scales[8 * c + e];
+      kz[e] = -8.0f * ksc[e];
+      vz[e] = -8.0f * vsc[e];
     }
   }
   float m_run[GH], l_run[GH];  // l_run: this lane's row group's tokens
@@ -442,14 +509,27 @@ __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float*
     float sc[GH][SB];
 #pragma unroll
     for (int i = 0; i < SB; ++i) {
-      float x[8];
-      kr[i].decode(ksc, x);
+      if constexpr (PK) {
+        uint32_t kp[4];
+        kr[i].pairs(ksc, kz, kp);
 #pragma unroll
-      for (int j = 0; j < GH; ++j) {
-        float d = q[j][0] * x[0];
+        for (int j = 0; j < GH; ++j) {
+          float d = dot2<DT>(kp[0], qp[j][0], 0.0f);
+          d = dot2<DT>(kp[1], qp[j][1], d);
+          d = dot2<DT>(kp[2], qp[j][2], d);
+          d = dot2<DT>(kp[3], qp[j][3], d);
+          sc[j][i] = group_sum<LPR>(d) * qs;
+        }
+      } else {
+        float x[8];
+        kr[i].decode(ksc, kz, x);
 #pragma unroll
-        for (int e = 1; e < 8; ++e) d = fmaf(q[j][e], x[e], d);
-        sc[j][i] = group_sum<LPR>(d);
+        for (int j = 0; j < GH; ++j) {
+          float d = q[j][0] * x[0];
+#pragma unroll
+          for (int e = 1; e < 8; ++e) d = fmaf(q[j][e], x[e], d);
+          sc[j][i] = group_sum<LPR>(d);
+        }
       }
     }
     if (a.mask) {  // additive mask, per head
@@ -499,9 +579,9 @@ __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float*
     for (int i = 0; i < SB; ++i) {
       float x[8];
       if constexpr (INT4)
-        vr[i].decode(vsc, x);
+        vr[i].decode(vsc, vz, x);
       else
-        vd[i].decode(vsc, x);
+        vd[i].decode(vsc, vz, x);
 #pragma unroll
       for (int j = 0; j < GH; ++j) {
         const float p = sc[j][i] == -INFINITY ? 0.0f : exp2f(sc[j][i] - m_new[j]);
