@@ -292,15 +292,6 @@ __device__ __forceinline__ float across_groups_max(float x) {
   return x;
 }
 
-// One wave per (query row, split).  LPR = head_dim / 8 lanes per K/V row,
-// TPS = 64 / LPR rows per wave load; lane (g = lane / LPR, c = lane % LPR)
-// holds query elements 8c .. 8c + 7 and, in step i of a 64-token chunk, token
-// chunk + TPS i + g.
-//
-// Workgroup order: a unit is (b, kv head, tq, split) and its G = Hq / Hkv
-// query heads read the same K/V rows.  Workgroups are dealt to the 8 XCDs
-// round-robin by id, so unit u goes to XCD u % 8 and its G waves take
-// consecutive slots there: the group shares one L2.
 // INT4 = true: K and V are INT4_SYM codes, dequantized as the codec's restore
 // does, (code - 8) * scale in fp32 rounded to DT (the dtype the restore would
 // write and q's dtype), so the scores see the values a decompressed tensor
@@ -420,6 +411,11 @@ struct RawRow<DT, true> {
 // (g = lane / LPR, c = lane % LPR) holds elements 8c .. 8c + 7 of the GH
 // query rows and, in step i of a batch, of K/V row t0 + TPS i + g, which it
 // loads (and for INT4 dequantizes) once for all GH heads.
+//
+// Workgroup order: a unit is (b, KV head, tq, split), served by G / GH
+// waves (G = Hq / Hkv).  Workgroups are dealt to the 8 XCDs round-robin by
+// id, so unit u goes to XCD u % 8 and its waves take consecutive slots
+// there: they share one L2.
 template <int DT, int LPR, bool INT4, int GH>
 __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float* part,
                                                               int64_t split_tokens,
