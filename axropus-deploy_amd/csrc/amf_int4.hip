@@ -55,16 +55,19 @@ __device__ __forceinline__ void load32(const uint8_t* p, float* x) {
 // CHANNEL = false: INT4_SYM_BLOCK (params: [n_pages] fp16);
 // CHANNEL = true : INT4_SYM       (params: [head_dim] fp16 per scale group).
 // One lane = one 8-element chunk (4 code bytes in, one 16-byte vector out):
-// wave-wide stores cover 1 KiB contiguously.
+// wave-wide stores cover 1 KiB contiguously.  A page of more than 8 passes
+// of the workgroup is cut into `parts` workgroups of whole passes (a dense
+// tensor's page can hold millions of elements).
 template <int DT, bool CHANNEL>
 __global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
     const uint64_t* __restrict__ code_planes, const uint64_t* __restrict__ param_planes,
     const uint64_t* __restrict__ cache_planes, int64_t cache_stride,
     const int32_t* __restrict__ block_ids, int64_t pool, int64_t n_pages, int n_planes,
-    SymGeom g, int32_t* err_flag) {
-  const PageWork pw = xcd_page_work(n_pages, n_planes);
+    int parts, SymGeom g, int32_t* err_flag) {
+  const PageWork pw = xcd_page_work(n_pages * parts, n_planes);
   if (!pw.valid) return;
-  const int64_t j = pw.j;
+  const int64_t j = pw.j / parts;
+  const int part = (int)(pw.j % parts);
   const int plane = pw.plane;
   const int64_t dp = block_ids ? (int64_t)block_ids[j] : j;
   if (dp < 0 || dp >= pool) {
@@ -73,6 +76,10 @@ __global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
   }
   const int page_elems = g.n_rows * g.head_dim;
   const int n8 = page_elems >> 3;
+  // this workgroup's chunks: [k_begin, k_end), k_begin a multiple of kThreads
+  const int span = (n8 + parts - 1) / parts;
+  const int k_begin = part * ((span + kThreads - 1) / kThreads * kThreads);
+  const int k_end = min(n8, k_begin + (span + kThreads - 1) / kThreads * kThreads);
   const uint32_t* __restrict__ codes =
       reinterpret_cast<const uint32_t*>(code_planes[plane]) + j * (int64_t)n8;
   const _Float16* __restrict__ params = reinterpret_cast<const _Float16*>(param_planes[plane]);
@@ -88,17 +95,17 @@ __global__ __launch_bounds__(kThreads) void int4_sym_dequant_scatter_kernel(
     for (int q = 0; q < 8; ++q) s_ch[q] = (float)params[d0 + q];
   }
   constexpr int U = AMF_SYM_RESTORE_UNROLL;
-  for (int base = tid; base < n8; base += U * kThreads) {
+  for (int base = k_begin + tid; base < k_end; base += U * kThreads) {
     uint32_t c[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = base + u * kThreads;
-      if (k < n8) c[u] = ld_stream(codes + k);
+      if (k < k_end) c[u] = ld_stream(codes + k);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = base + u * kThreads;
-      if (k < n8) {
+      if (k < k_end) {
         float x[8];
 #pragma unroll
         for (int n = 0; n < 8; ++n) x[n] = (nib(c[u], n) - 8.0f) * (CHANNEL ? s_ch[n] : s_page);
@@ -751,7 +758,6 @@ extern "C" int amf_int4_dequant_scatter(int32_t format, const uint64_t* code_pla
   if (n_pages * n_planes > 0x7FFFFFF0ll)
     return fail(AMF_ERR_UNSUPPORTED, "%s: %lld pages x %d planes exceed one launch", who,
                 (long long)n_pages, n_planes);
-  const dim3 grid = xcd_page_grid(n_pages, n_planes);
   if (format == AMF_FMT_INT4_ASYM_G32) {
     AsymGeom g;
     size_t lds_staged, lds_tables;
@@ -772,10 +778,17 @@ extern "C" int amf_int4_dequant_scatter(int32_t format, const uint64_t* code_pla
   if (ch && (8 * kThreads) % head_dim != 0)
     return fail(AMF_ERR_UNSUPPORTED, "%s: head_dim %d must divide %d", who, head_dim, 8 * kThreads);
   if (n_pages == 0) return ok();
+  // pages beyond 8 workgroup passes are split over workgroups of 8 passes
+  const int64_t n8 = (int64_t)g.n_rows * g.head_dim / 8;
+  const int parts = (int)std::max<int64_t>(1, n8 / (8 * kThreads));
+  if (n_pages * parts * n_planes > 0x7FFFFFF0ll)
+    return fail(AMF_ERR_UNSUPPORTED, "%s: %lld pages x %d parts x %d planes exceed one launch",
+                who, (long long)n_pages, parts, n_planes);
+  const dim3 sgrid = xcd_page_grid(n_pages * parts, n_planes);
 #define AMF_LAUNCH(C)                                                                        \
-  int4_sym_dequant_scatter_kernel<DT, C><<<grid, kThreads, 0, s>>>(                           \
+  int4_sym_dequant_scatter_kernel<DT, C><<<sgrid, kThreads, 0, s>>>(                          \
       code_planes, param_planes, cache_planes, cache_page_stride, block_ids, pool_pages,      \
-      n_pages, n_planes, g, err_flag)
+      n_pages, n_planes, parts, g, err_flag)
   AMF_WITH_DTYPE(cache_dtype, if (ch) AMF_LAUNCH(true); else AMF_LAUNCH(false));
 #undef AMF_LAUNCH
   return check_launch(who);
