@@ -194,3 +194,77 @@ def test_decode_entry_refuses_host_tensors():
     k = torch.randn(1, 2, 8, 64)
     with pytest.raises(RuntimeError, match="GPU"):
         int4_decode_attention(q, k, k)
+
+
+# ---- positional attention: which CompressedKV the in-place INT4 kernel takes --
+
+
+def _int4_sym_kv(shape, device="cpu"):
+    """A CompressedKV shaped as the int4_sym codec leaves one: codes uint8
+    [*shape[:-1], D / 2] and fp16 scales [D] (values irrelevant here)."""
+    from korith_vllm_ext.codecs import CompressedKV
+
+    D = shape[-1]
+    return CompressedKV(format="int4_sym",
+                        data=torch.zeros(*shape[:-1], D // 2, dtype=torch.uint8, device=device),
+                        scales=torch.ones(D, dtype=torch.float16, device=device), shape=shape,
+                        dtype_original=torch.bfloat16)
+
+
+def test_int4_sym_operands_accepts_the_codec_layout_only():
+    """_int4_sym_operands (kernels/dispatch.py) hands the in-place kernel the
+    codes and scales only when they are laid out as the codec writes them,
+    on q's device, with q's lead dims; anything else is None (the caller
+    then restores and runs the dense kernel)."""
+    from korith_vllm_ext.codecs import CompressedKV
+    from korith_vllm_ext.kernels.dispatch import _int4_sym_operands
+
+    q = torch.zeros(2, 8, 1, 128, dtype=torch.bfloat16)
+    good = _int4_sym_kv((2, 4, 300, 128))
+    ops = _int4_sym_operands(good, q)
+    assert ops is not None and ops[0] is good.data and ops[1] is good.scales
+    # other formats, plain tensors
+    fp8 = CompressedKV(format="fp8_e4m3", data=good.data, scales=good.scales, shape=good.shape)
+    assert _int4_sym_operands(fp8, q) is None
+    assert _int4_sym_operands(torch.zeros(2, 4, 300, 128), q) is None
+    # lead dims or head_dim not q's
+    assert _int4_sym_operands(_int4_sym_kv((3, 4, 300, 128)), q) is None
+    assert _int4_sym_operands(_int4_sym_kv((2, 4, 300, 64)), q) is None
+    assert _int4_sym_operands(_int4_sym_kv((4, 300, 128)), q) is None
+    # codes: wrong dtype, shape or a non-contiguous view
+    bad = _int4_sym_kv((2, 4, 300, 128))
+    bad.data = bad.data.to(torch.int8)
+    assert _int4_sym_operands(bad, q) is None
+    bad = _int4_sym_kv((2, 4, 300, 128))
+    bad.data = torch.zeros(2, 4, 300, 128, dtype=torch.uint8)
+    assert _int4_sym_operands(bad, q) is None
+    bad = _int4_sym_kv((2, 4, 300, 128))
+    bad.data = torch.zeros(2, 4, 64, 300, dtype=torch.uint8).transpose(-1, -2)
+    assert _int4_sym_operands(bad, q) is None
+    # scales: wrong dtype or count
+    bad = _int4_sym_kv((2, 4, 300, 128))
+    bad.scales = bad.scales.float()
+    assert _int4_sym_operands(bad, q) is None
+    bad = _int4_sym_kv((2, 4, 300, 128))
+    bad.scales = torch.ones(64, dtype=torch.float16)
+    assert _int4_sym_operands(bad, q) is None
+
+
+def test_int4_sym_attention_declines_without_launching():
+    """int4_sym_attention returns None before any device work for head dims
+    the split kernel does not take and for K/V it cannot read in place."""
+    from korith_vllm_ext.kernels.dispatch import int4_sym_attention
+
+    q80 = torch.zeros(1, 4, 1, 80, dtype=torch.bfloat16)
+    assert int4_sym_attention(q80, _int4_sym_kv((1, 4, 16, 80)), _int4_sym_kv((1, 4, 16, 80)),
+                              None, None) is None
+    q = torch.zeros(1, 4, 1, 128, dtype=torch.int32)
+    assert int4_sym_attention(q, _int4_sym_kv((1, 4, 16, 128)), _int4_sym_kv((1, 4, 16, 128)),
+                              None, None) is None
+    q = torch.zeros(1, 4, 1, 128, dtype=torch.bfloat16)
+    k = _int4_sym_kv((1, 4, 16, 128))
+    assert int4_sym_attention(q, k, _int4_sym_kv((1, 4, 17, 128)), None, None) is None
+    assert int4_sym_attention(q, k, torch.zeros(1, 4, 16, 128), None, None) is None
+    # GQA needs the query heads to be a multiple of the KV heads
+    q3 = torch.zeros(1, 6, 1, 128, dtype=torch.bfloat16)
+    assert int4_sym_attention(q3, k, k, None, None) is None
