@@ -508,7 +508,7 @@ __device__ __forceinline__ void chunk_qk(
     const uint8_t* slot, const bool (&pok)[2], int c0, int tok_end, int lo, int hi,
     const u32x4 (&qa)[(R + 3) / 4][4], float qk_scale, const float (&qs_lds)[(R + 3) / 4][4][4],
     float (&m_run)[(R + 3) / 4], float (&l_run)[(R + 3) / 4],
-    float (&corr)[(R + 3) / 4], float (&wsum)[(R + 3) / 4], float (&lb)[(R + 3) / 4],
+    float (&corr)[(R + 3) / 4], float (&wsum)[(R + 3) / 4], float (&lsum)[(R + 3) / 4],
     f32x4 (&acc)[(R + 3) / 4][8], float (&p_lds)[(R + 3) / 4][2][4][16]) {
   constexpr int NT = (R + 3) / 4;
   const int lane = lo + 16 * hi;
@@ -567,11 +567,11 @@ __device__ __forceinline__ void chunk_qk(
       l_run[T] *= alpha;
 #pragma unroll
       for (int b = 0; b < 8; ++b) acc[T][b] *= alpha;
-      // corr, wsum and lb live in the A layout: lane lo holds head 4T + lo/4.
+      // corr, wsum and lsum live in the A layout: lane lo holds head 4T + lo/4.
       const float alpha_a = __shfl(alpha, 16 * (lo >> 2));
       corr[T] *= alpha_a;
       wsum[T] *= alpha_a;
-      lb[T] *= alpha_a;
+      lsum[T] *= alpha_a;
       m_run[T] = m_new;
     }
     p[T][0] = exp2_fast(x[T][0] - m_run[T]);
@@ -606,24 +606,34 @@ __device__ __forceinline__ void chunk_qk(
 // below allows, else the fp16 pair; AMF_DECODE_MFMA_PRECISE takes the pair
 // throughout.
 //
+// Centered codes.  The fp16 forms multiply the weights by the codes c in
+// [0, 15] but account for them as c - 8 in [-8, 7]: each chunk subtracts
+// 8 * (the sum of the weights exactly as the MFMA used them, the fp16
+// values for the fp16 form) from the row-group's zero-point term and adds
+// 8 s to each token's zero point instead (z + 8 s is exact in fp32).  The
+// total is unchanged, but the weights' rounding error now meets |c - 8| <= 8
+// instead of c <= 15.
+//
 // Error bound of the fp16 form.  Rounding w to fp16 is off by at most
 // 2^-11 (w + 2^-14) (relative 2^-11 for a normal result, 2^-25 absolute for
 // a subnormal one), so the fp16 weights move output element d of row (r, g)
-// by at most 2^-11 * 15 * W / l, with codes c <= 15, W the sum of w + 2^-14
-// over the row-group's fp16 weights and l the row's softmax sum (every
-// chunk's tokens).  A chunk takes the fp16 form only if W <= kPv16Beta * l
-// holds afterwards for every row-group of the GQA group; then that error is
-// at most 2^-11 * 15 * kPv16Beta = 0.0147 for the finished row (both sides
+// by at most 2^-11 * 8 * W / l, with centered codes |c - 8| <= 8, W the sum
+// of w + 2^-14 over the row-group's fp16 weights and l the row's softmax sum
+// (every chunk's tokens).  A chunk takes the fp16 form only if
+// W <= kPv16Beta * l holds afterwards for every row-group of the GQA group;
+// then that error is at most 2^-11 * 8 * kPv16Beta = 0.0146 for the finished
+// row (both sides
 // scale alike under the online rescale, l only grows and W only by accepted
 // chunks) and for an LSE merge of such rows.  The check: lane (lo, hi) keeps
-// its k-slice's share of W; a chunk passes at once if every lane's share
-// stays <= kPv16Beta / 4 * lb, lb a lower bound of l (l when last taken,
-// rescaled alike), as the four shares then add up to at most kPv16Beta * l;
-// otherwise the shares are added across the k-slices and compared with the
-// current l (a row sum of l_run).  The weights' fp16 values stand in for w in
-// W (off by 2^-11 relative, inside the bound's rounding of 0.0147 to 0.015).
+// its k-slice's shares of W and of l (the p of its tokens 8 hi .. 8 hi + 7 of
+// every chunk); a chunk passes at once if every lane's W share stays within
+// kPv16Beta times its l share, as the four lanes of a row-group then add up
+// to W <= kPv16Beta * l; otherwise the shares are added across the k-slices
+// and compared.  The weights' fp16 values stand in for w in W, and the l
+// shares are summed in another order than l_run (off by 2^-11 and a few fp32
+// ulps relative, inside the bound's rounding of 0.0146 to 0.015).
 #ifndef AMF_DECODE_PV16_BETA
-#define AMF_DECODE_PV16_BETA 2.0f
+#define AMF_DECODE_PV16_BETA 3.75f
 #endif
 constexpr float kPv16Beta = AMF_DECODE_PV16_BETA;
 
@@ -651,7 +661,9 @@ __device__ __forceinline__ void pv_weights_f16(const u32x4& vp0, const u32x4& vp
                                                float (&p_lds)[(R + 3) / 4][2][4][16],
                                                u32x4 (&a16)[(R + 3) / 4],
                                                f16x2_t (&h16)[(R + 3) / 4][4],
-                                               float (&corr)[(R + 3) / 4]) {
+                                               float (&corr)[(R + 3) / 4],
+                                               float (&wx)[(R + 3) / 4],
+                                               float (&lsum)[(R + 3) / 4]) {
   constexpr int NT = (R + 3) / 4;
   const int vu = hi >> 1, vhalf = hi & 1;
   const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
@@ -660,14 +672,18 @@ __device__ __forceinline__ void pv_weights_f16(const u32x4& vp0, const u32x4& vp
     const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
     const float4 pa = pl[0], pb = pl[1];
     const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+    lsum[T] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
     float w[8];
-    float cs = corr[T];
+    float cs = corr[T], ws = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float sv = pscale(pw[e]);
       w[e] = mul_legacy(pv[e], (e & 1) ? sv : sv * 16.0f);
-      cs += mul_legacy(pv[e], pzero(pw[e]));
+      // centered codes: the zero point carries + 8 s
+      cs += mul_legacy(pv[e], pzero(pw[e]) + 8.0f * sv);
+      ws += (e & 1) ? w[e] : w[e] * 0.0625f;
     }
+    wx[T] = ws;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       h16[T][j] = __builtin_convertvector((f32x2_t){w[j], w[j + 4]}, f16x2_t);
@@ -678,13 +694,14 @@ __device__ __forceinline__ void pv_weights_f16(const u32x4& vp0, const u32x4& vp
 }
 
 // The error bound above for the chunk's fp16 weights; on yes, they join
-// wsum (the lane's share of W).  lb holds the lower bound of l per lane (A
-// layout, head 4T + lo/4).
+// wsum (the lane's share of W).  lsum holds the lane's share of l (A layout,
+// head 4T + lo/4).  wr returns the chunk's fp16 weight sum per lane, for the
+// centered-code correction.
 template <int R>
 __device__ __forceinline__ bool pv_single_ok(int lo, const f16x2_t (&h16)[(R + 3) / 4][4],
-                                             const float (&l_run)[(R + 3) / 4],
                                              float (&wsum)[(R + 3) / 4],
-                                             float (&lb)[(R + 3) / 4]) {
+                                             const float (&lsum)[(R + 3) / 4],
+                                             float (&wr)[(R + 3) / 4]) {
   constexpr int NT = (R + 3) / 4;
   const f16x2_t k_even = {(_Float16)0.0625f, (_Float16)0.0625f}, k_odd = {(_Float16)1.0f,
                                                                           (_Float16)1.0f};
@@ -692,14 +709,17 @@ __device__ __forceinline__ bool pv_single_ok(int lo, const f16x2_t (&h16)[(R + 3
   bool ok = true;
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
-    // the lane's 8 weights (pairs 0, 2 hold 16 w of even tokens) + 8 * 2^-14
-    float d = __builtin_amdgcn_fdot2(h16[T][1], k_odd, wsum[T] + 0x1p-11f, false);
+    // the lane's 8 weights as fp16 (pairs 0, 2 hold 16 w of even tokens),
+    // then with the lane's share so far and 8 * 2^-14
+    float d = __builtin_amdgcn_fdot2(h16[T][1], k_odd, 0.0f, false);
     d = __builtin_amdgcn_fdot2(h16[T][3], k_odd, d, false);
     d = __builtin_amdgcn_fdot2(h16[T][0], k_even, d, false);
-    cand[T] = __builtin_amdgcn_fdot2(h16[T][2], k_even, d, false);
+    d = __builtin_amdgcn_fdot2(h16[T][2], k_even, d, false);
+    wr[T] = d;
+    cand[T] = d + (wsum[T] + 0x1p-11f);
     // rows past the GQA group carry scores of a zero query: never checked
     const bool row_used = 4 * T + (lo >> 2) < R;
-    ok = ok && (!row_used || cand[T] <= (0.25f * kPv16Beta) * lb[T]);
+    ok = ok && (!row_used || cand[T] <= kPv16Beta * lsum[T]);
   }
   if (__any(!ok)) {
     ok = true;
@@ -707,10 +727,10 @@ __device__ __forceinline__ bool pv_single_ok(int lo, const f16x2_t (&h16)[(R + 3
     for (int T = 0; T < NT; ++T) {
       float wrow = cand[T] + __shfl_xor(cand[T], 16);
       wrow += __shfl_xor(wrow, 32);
-      // l of head 4T + lo/4: a row sum of the C layout (head 4T + hi), fetched
-      lb[T] = __shfl(row_sum16(l_run[T]), 16 * (lo >> 2));
+      float lrow = lsum[T] + __shfl_xor(lsum[T], 16);
+      lrow += __shfl_xor(lrow, 32);
       const bool row_used = 4 * T + (lo >> 2) < R;
-      ok = ok && (!row_used || wrow <= kPv16Beta * lb[T]);
+      ok = ok && (!row_used || wrow <= kPv16Beta * lrow);
     }
     if (__any(!ok)) return false;
   }
@@ -965,7 +985,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     __builtin_amdgcn_wave_barrier();
 
 
-    float m_run[NT], l_run[NT], corr[NT], wsum[NT], lb[NT];
+    float m_run[NT], l_run[NT], corr[NT], wsum[NT], lsum[NT];
     f32x4 acc[NT][8];
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
@@ -973,7 +993,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
       l_run[T] = 0.0f;
       corr[T] = 0.0f;
       wsum[T] = 0.0f;
-      lb[T] = 0.0f;
+      lsum[T] = 0.0f;
 #pragma unroll
       for (int b = 0; b < 8; ++b) acc[T][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -1003,7 +1023,7 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
         split_page(spg, pi0 + 2 * c, &pok[0]);
         split_page(spg, pi0 + 2 * c + 1, &pok[1]);
         chunk_qk<R>(ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa, qk_scale, qs_lds,
-                    m_run, l_run, corr, wsum, lb, acc, p_lds);
+                    m_run, l_run, corr, wsum, lsum, acc, p_lds);
       };
       // Chunks take fp16 weights, single where the error bound allows
       // (pv_single_ok) and paired elsewhere, until one whose V scales fp16
@@ -1022,11 +1042,18 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
         }
         u32x4 a16[NT];
         f16x2_t h16[NT][4];
-        pv_weights_f16<R>(vp0, vp1, lo, hi, p_lds, a16, h16, corr);
-        if (a.pv16 && pv_single_ok<R>(lo, h16, l_run, wsum, lb))
+        float wx[NT], wr[NT];
+        pv_weights_f16<R>(vp0, vp1, lo, hi, p_lds, a16, h16, corr, wx, lsum);
+        // centered codes: take 8 x the weights the MFMA uses off the zero-point term
+        if (a.pv16 && pv_single_ok<R>(lo, h16, wsum, lsum, wr)) {
+#pragma unroll
+          for (int T = 0; T < NT; ++T) corr[T] = __builtin_fmaf(-8.0f, wr[T], corr[T]);
           chunk_pv_f16<R>(ring[c % D], lane, a16, acc);
-        else
+        } else {
+#pragma unroll
+          for (int T = 0; T < NT; ++T) corr[T] = __builtin_fmaf(-8.0f, wx[T], corr[T]);
           chunk_pv_f16_pair<R>(ring[c % D], lo, hi, p_lds, acc);
+        }
       }
       for (; c < nch; ++c) {
         if (!pending) {
