@@ -212,18 +212,34 @@ __device__ __forceinline__ void pk_bf16_hilo(float a, float b, uint32_t* hi, uin
   *lo = pk_bf16(a - u2f(h << 16), b - u2f(h & 0xFFFF0000u));
 }
 
-// a * b with +0 * x = +0 for every x (v_mul_legacy_f32); otherwise IEEE.
-__device__ __forceinline__ float mul_legacy(float a, float b) {
-  float r;
-  asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-
 __device__ __forceinline__ float pscale(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
 }
 __device__ __forceinline__ float pzero(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// h's high (fma_mix_hi, mul_mix_hi) or low (mul_mix_lo) fp16 half times x,
+// plus c (or +0), as one v_fma_mix_f32 (the fp16 operand converts exactly;
+// one rounding).  Written out because the compiler converts a param it uses
+// twice and then issues a separate fma for each use.  No operand may be an
+// MFMA result: the compiler does not insert the wait states such a result
+// needs before an inline-asm read.
+__device__ __forceinline__ float fma_mix_hi(uint32_t h, float x, float c) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=v"(r) : "v"(h), "v"(x), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float mul_mix_hi(uint32_t h, float x) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+  return r;
+}
+__device__ __forceinline__ float mul_mix_lo(uint32_t h, float x) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+  return r;
 }
 
 // Query element as fp32 (bf16 or fp16 storage).
@@ -370,12 +386,22 @@ __device__ __forceinline__ int64_t page_of(const DecodeArgs& a, const int32_t* b
 // (no bank conflicts).  No load registers are held while a chunk is in
 // flight, so a wave keeps several chunks in flight at any occupancy.
 constexpr int kSlotBytes = 5120;
-constexpr int kDmaNonTemporal = 2;  // aux bits of the LDS DMA: nt
 
+// One 16-byte LDS DMA per lane: lane i's 16 bytes at g land at lds + 16 i
+// (lds wave-uniform), non-temporal.  Written as inline asm so that the
+// compiler does not track it: it cannot tell which LDS bytes a DMA writes,
+// and for a DMA it knows of it waits for every load in flight (vmcnt(0))
+// before LDS accesses it cannot separate from it (p_lds, and the ring slot
+// being read), which drains the ring each chunk.  dma_wait does the waiting
+// instead; loads the compiler issues complete in order with these DMAs, so
+// its own vmcnt waits stay valid (DMAs it does not count only make them
+// wait longer).  M0 holds the LDS address; one wait state separates its
+// write from the DMA.
 __device__ __forceinline__ void lds_dma16(const void* g, uint8_t* lds) {
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(g),
-                                   (__attribute__((address_space(3))) uint32_t*)lds, 16, 0,
-                                   kDmaNonTemporal);
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+               : : "v"(g), "s"(m0) : "memory", "m0");
 }
 
 __device__ __forceinline__ void dma_chunk(const DecodeArgs& a, int64_t pg0, int64_t pg1, int h,
@@ -462,6 +488,11 @@ __device__ __forceinline__ SplitPages split_pages(const DecodeArgs& a, int raw, 
   SplitPages sp;
   sp.first = tok_begin / kBS;
   const int n = (tok_end - tok_begin + kBS - 1) / kBS;
+  // An empty asm that reads raw outside any lane branch: the compiler waits
+  // for raw's load here, on every path.  Otherwise the wait sits in a branch
+  // it cannot prove is taken, and it later waits for every load and DMA in
+  // flight (vmcnt(0)) before it reuses raw's register, inside the chunk loop.
+  asm volatile("" : : "v"(raw));
   int v = -1;
   if ((int)(threadIdx.x & 63) < n) {
     v = raw;
@@ -524,12 +555,9 @@ __device__ __forceinline__ void chunk_qk(
     u32x4 kb[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) kb[st] = nib8_to_f16_sub(kcode[u][st]);
-    float ks[4], kz[4];
+    float ks[4];
 #pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
-      ks[gi] = pscale(kpar[u][gi]);
-      kz[gi] = pzero(kpar[u][gi]);
-    }
+    for (int gi = 0; gi < 4; ++gi) ks[gi] = pscale(kpar[u][gi]);
     const bool valid = pok[u] && (c0 + u * kBS + lo) < tok_end;
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
@@ -539,14 +567,14 @@ __device__ __forceinline__ void chunk_qk(
       f32x4 cacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int st = 0; st < 4; ++st) cacc = mfma_f16(qa[T][st], kb[st], cacc);
-      // One fma chain over the four groups (no zero seed: -0 + 0 would not fold).
-      float sc = kz[0] * qsum[0];
-      sc = __builtin_fmaf(ks[0], cacc[0], sc);
+      // One fma chain: the zero-point terms (the zeros read as fp16 from the
+      // high halves of the param words), then the four scaled group sums
+      // (cacc, an MFMA result, is read by compiler-visible fmas only).
+      float sc = mul_mix_hi(kpar[u][0], qsum[0]);
 #pragma unroll
-      for (int gi = 1; gi < 4; ++gi) {
-        sc = __builtin_fmaf(kz[gi], qsum[gi], sc);
-        sc = __builtin_fmaf(ks[gi], cacc[gi], sc);
-      }
+      for (int gi = 1; gi < 4; ++gi) sc = fma_mix_hi(kpar[u][gi], qsum[gi], sc);
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) sc = __builtin_fmaf(ks[gi], cacc[gi], sc);
       x[T][u] = valid ? sc * qk_scale : -__builtin_inff();
     }
   }
@@ -637,6 +665,18 @@ __device__ __forceinline__ void chunk_qk(
 #endif
 constexpr float kPv16Beta = AMF_DECODE_PV16_BETA;
 
+// Sum of a lane's 8 fp16 PV weights as the MFMA takes them: pairs 0 and 2
+// hold 16 w of even tokens, pairs 1 and 3 w of odd ones (fp16 products are
+// exact in the fp32 sum).
+__device__ __forceinline__ float f16_weight_sum(const f16x2_t (&h)[4]) {
+  const f16x2_t k_even = {(_Float16)0.0625f, (_Float16)0.0625f}, k_odd = {(_Float16)1.0f,
+                                                                          (_Float16)1.0f};
+  float d = __builtin_amdgcn_fdot2(h[1], k_odd, 0.0f, false);
+  d = __builtin_amdgcn_fdot2(h[3], k_odd, d, false);
+  d = __builtin_amdgcn_fdot2(h[0], k_even, d, false);
+  return __builtin_amdgcn_fdot2(h[2], k_even, d, false);
+}
+
 // Whether a chunk's V scales allow fp16 weights (0 or in [2^-10, 15.5]: no
 // weight overflows fp16 with p <= 2^8, and every token with p >= 2^-4 has a
 // normal weight): each lane checks the scale words of its 8 tokens, then the
@@ -648,25 +688,47 @@ __device__ __forceinline__ bool pv_f16_range_ok(const u32x4& vp0, const u32x4& v
   return !__any(smax > kF16ScaleMaxBits || (smax != 0u && smax < kF16ScaleMinBits));
 }
 
+// Zeroes the V param words of the lane's tokens 8 hi .. 8 hi + 7 that lie
+// outside the context or on a page with a bad id (their bytes may be
+// anything), for a chunk that holds such tokens; the fp16 weight path then
+// multiplies them by p = +0 with plain IEEE operations.
+__device__ __forceinline__ void mask_vp_invalid(u32x4& vp0, u32x4& vp1, const bool (&pok)[2],
+                                                int c0, int tok_end, int hi) {
+  const int t0 = c0 + 8 * hi;
+  const bool pg = pok[hi >> 1];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    vp0[e] = (pg && t0 + e < tok_end) ? vp0[e] : 0u;
+    vp1[e] = (pg && t0 + 4 + e < tok_end) ? vp1[e] : 0u;
+  }
+}
+
 // The chunk's fp16 PV operand in the A layout: lane (lo, hi) holds row-group
 // (head 4T + lo/4, group lo%4) for tokens 8 hi .. 8 hi + 7 of the chunk, in
 // the operand order [t0 t4 t1 t5 t2 t6 t3 t7], 16 w for even and w for odd
-// tokens (also as fp16 pairs in h16, the operand's dwords); the zero-point
-// sum p * z goes to corr.  A token outside the
-// context or on a page with a bad id has p = +0 exactly (its score is -inf);
-// its param words may hold any bytes, and the legacy multiply (+0 * x = +0
-// for every x, NaN and infinities included) keeps them out.
+// tokens.  The zero-point sum p * (z + 8 s) goes to corr, the lane's p to
+// lsum (its share of l), and wr returns the lane's fp16 weights summed as
+// the MFMA takes them (w, with the 16 of even tokens divided out), for the
+// centered-code correction and the error bound.  The param words of tokens
+// outside the context are zero (mask_vp_invalid), and those tokens have
+// p = +0 exactly (their score is -inf).
 template <int R>
 __device__ __forceinline__ void pv_weights_f16(const u32x4& vp0, const u32x4& vp1, int lo, int hi,
                                                float (&p_lds)[(R + 3) / 4][2][4][16],
                                                u32x4 (&a16)[(R + 3) / 4],
-                                               f16x2_t (&h16)[(R + 3) / 4][4],
                                                float (&corr)[(R + 3) / 4],
-                                               float (&wx)[(R + 3) / 4],
-                                               float (&lsum)[(R + 3) / 4]) {
+                                               float (&lsum)[(R + 3) / 4],
+                                               float (&wr)[(R + 3) / 4]) {
   constexpr int NT = (R + 3) / 4;
   const int vu = hi >> 1, vhalf = hi & 1;
   const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
+  // per token: 16 s for even tokens, and the centered zero point z + 8 s
+  float s16[8], z8[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    s16[e] = pscale(pw[e]) * 16.0f;
+    z8[e] = pzero(pw[e]) + 8.0f * pscale(pw[e]);
+  }
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
     const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
@@ -674,49 +736,37 @@ __device__ __forceinline__ void pv_weights_f16(const u32x4& vp0, const u32x4& vp
     const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
     lsum[T] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
     float w[8];
-    float cs = corr[T], ws = 0.0f;
+    float cs = corr[T];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float sv = pscale(pw[e]);
-      w[e] = mul_legacy(pv[e], (e & 1) ? sv : sv * 16.0f);
-      // centered codes: the zero point carries + 8 s
-      cs += mul_legacy(pv[e], pzero(pw[e]) + 8.0f * sv);
-      ws += (e & 1) ? w[e] : w[e] * 0.0625f;
+      w[e] = (e & 1) ? mul_mix_lo(pw[e], pv[e]) : pv[e] * s16[e];
+      cs = __builtin_fmaf(pv[e], z8[e], cs);
     }
-    wx[T] = ws;
+    f16x2_t h16[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      h16[T][j] = __builtin_convertvector((f32x2_t){w[j], w[j + 4]}, f16x2_t);
-      a16[T][j] = __builtin_bit_cast(uint32_t, h16[T][j]);
+      h16[j] = __builtin_convertvector((f32x2_t){w[j], w[j + 4]}, f16x2_t);
+      a16[T][j] = __builtin_bit_cast(uint32_t, h16[j]);
     }
     corr[T] = cs;
+    wr[T] = f16_weight_sum(h16);
   }
 }
 
-// The error bound above for the chunk's fp16 weights; on yes, they join
-// wsum (the lane's share of W).  lsum holds the lane's share of l (A layout,
-// head 4T + lo/4).  wr returns the chunk's fp16 weight sum per lane, for the
-// centered-code correction.
+// The error bound above for the chunk's fp16 weights (wr, the lane's sum of
+// them); on yes, they join wsum (the lane's share of W).  lsum holds the
+// lane's share of l (A layout, head 4T + lo/4).
 template <int R>
-__device__ __forceinline__ bool pv_single_ok(int lo, const f16x2_t (&h16)[(R + 3) / 4][4],
+__device__ __forceinline__ bool pv_single_ok(int lo, const float (&wr)[(R + 3) / 4],
                                              float (&wsum)[(R + 3) / 4],
-                                             const float (&lsum)[(R + 3) / 4],
-                                             float (&wr)[(R + 3) / 4]) {
+                                             const float (&lsum)[(R + 3) / 4]) {
   constexpr int NT = (R + 3) / 4;
-  const f16x2_t k_even = {(_Float16)0.0625f, (_Float16)0.0625f}, k_odd = {(_Float16)1.0f,
-                                                                          (_Float16)1.0f};
   float cand[NT];
   bool ok = true;
 #pragma unroll
   for (int T = 0; T < NT; ++T) {
-    // the lane's 8 weights as fp16 (pairs 0, 2 hold 16 w of even tokens),
-    // then with the lane's share so far and 8 * 2^-14
-    float d = __builtin_amdgcn_fdot2(h16[T][1], k_odd, 0.0f, false);
-    d = __builtin_amdgcn_fdot2(h16[T][3], k_odd, d, false);
-    d = __builtin_amdgcn_fdot2(h16[T][0], k_even, d, false);
-    d = __builtin_amdgcn_fdot2(h16[T][2], k_even, d, false);
-    wr[T] = d;
-    cand[T] = d + (wsum[T] + 0x1p-11f);
+    // the lane's share so far, the chunk's weights and 8 * 2^-14
+    cand[T] = wr[T] + (wsum[T] + 0x1p-11f);
     // rows past the GQA group carry scores of a zero query: never checked
     const bool row_used = 4 * T + (lo >> 2) < R;
     ok = ok && (!row_used || cand[T] <= kPv16Beta * lsum[T]);
@@ -758,18 +808,23 @@ __device__ __forceinline__ void chunk_pv_f16(const uint8_t* slot, int lane,
   __builtin_amdgcn_wave_barrier();
 }
 
-// PV of one chunk with fp16 pairs, from the weights in p_lds and the slot's V
-// operands (the zero-point sum has been added).  One 16-row tile at a time,
-// so that one tile's pair is live (the code operand is rebuilt per tile).
+// The second half of a chunk's fp16 pair (after chunk_pv_f16 with the
+// single weights, which are the pair's hi parts): lo = fp16(w - hi) from the
+// weights in p_lds and the V params (masked as for pv_weights_f16) and the
+// slot's V codes, its PV product, and 8 x its
+// weights off the zero-point term (centered codes).  One 16-row tile at a
+// time, so that one tile's operand is live (the code operand is rebuilt per
+// tile).
 template <int R>
-__device__ __forceinline__ void chunk_pv_f16_pair(const uint8_t* slot, int lo, int hi,
-                                                  float (&p_lds)[(R + 3) / 4][2][4][16],
-                                                  f32x4 (&acc)[(R + 3) / 4][8]) {
+__device__ __forceinline__ void chunk_pv_f16_lo(const uint8_t* slot, const u32x4& vp0,
+                                                const u32x4& vp1, int lo, int hi,
+                                                float (&p_lds)[(R + 3) / 4][2][4][16],
+                                                float (&corr)[(R + 3) / 4],
+                                                f32x4 (&acc)[(R + 3) / 4][8]) {
   constexpr int NT = (R + 3) / 4;
   const int lane = lo + 16 * hi;
-  u32x4 vc0, vc1, vp0, vp1;
+  u32x4 vc0, vc1;
   read_chunk_vc(slot, lane, &vc0, &vc1);
-  read_chunk_vp(slot, lane, &vp0, &vp1);
   const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
   const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
   const int vu = hi >> 1, vhalf = hi & 1;
@@ -778,39 +833,42 @@ __device__ __forceinline__ void chunk_pv_f16_pair(const uint8_t* slot, int lo, i
     const float4* pl = reinterpret_cast<const float4*>(&p_lds[T][vu][lo >> 2][8 * vhalf]);
     const float4 pa = pl[0], pb = pl[1];
     const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-    u32x4 ah, al;
+    u32x4 al;
+    f16x2_t l16[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // operand pair (t_j, t_{j+4}): 16 w for even tokens, w for odd ones
       const float sa = pscale(pw[j]), sb = pscale(pw[j + 4]);
-      const float wa = mul_legacy(pv[j], (j & 1) ? sa : sa * 16.0f);
-      const float wb = mul_legacy(pv[j + 4], (j & 1) ? sb : sb * 16.0f);
+      const float wa = pv[j] * ((j & 1) ? sa : sa * 16.0f);
+      const float wb = pv[j + 4] * ((j & 1) ? sb : sb * 16.0f);
       const uint32_t h = pk_f16(wa, wb);
-      ah[j] = h;
-      al[j] = pk_f16(wa - half_lo<false>(h), wb - half_hi<false>(h));
+      l16[j] = __builtin_convertvector(
+          (f32x2_t){wa - half_lo<false>(h), wb - half_hi<false>(h)}, f16x2_t);
+      al[j] = __builtin_bit_cast(uint32_t, l16[j]);
     }
+    corr[T] = __builtin_fmaf(-8.0f, f16_weight_sum(l16), corr[T]);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       const u32x4 vb = nib8_to_f16_sub(vw[b]);
-      acc[T][b] = mfma_f16(ah, vb, acc[T][b]);
       acc[T][b] = mfma_f16(al, vb, acc[T][b]);
     }
   }
   __builtin_amdgcn_wave_barrier();
 }
 
-// PV of one chunk with bf16 hi + lo weights; the zero-point term carries the
-// codes' bias, -128 s per token, besides the zero point p * z.
+// PV of one chunk with bf16 hi + lo weights, from the V params (masked as for
+// pv_weights_f16); the zero-point term carries the codes' bias, -128 s per
+// token, besides the zero point p * z.
 template <int R>
-__device__ __forceinline__ void chunk_pv_bf16(const uint8_t* slot, int lo, int hi,
+__device__ __forceinline__ void chunk_pv_bf16(const uint8_t* slot, const u32x4& vp0,
+                                              const u32x4& vp1, int lo, int hi,
                                               float (&corr)[(R + 3) / 4],
                                               f32x4 (&acc)[(R + 3) / 4][8],
                                               float (&p_lds)[(R + 3) / 4][2][4][16]) {
   constexpr int NT = (R + 3) / 4;
   const int vu = hi >> 1, vhalf = hi & 1;
-  u32x4 vc0, vc1, vp0, vp1;
+  u32x4 vc0, vc1;
   read_chunk_vc(slot, lo + 16 * hi, &vc0, &vc1);
-  read_chunk_vp(slot, lo + 16 * hi, &vp0, &vp1);
   const uint32_t pw[8] = {vp0[0], vp0[1], vp0[2], vp0[3], vp1[0], vp1[1], vp1[2], vp1[3]};
   const uint32_t vw[8] = {vc0[0], vc0[1], vc0[2], vc0[3], vc1[0], vc1[1], vc1[2], vc1[3]};
   u32x4 ahi[NT], alo[NT];
@@ -824,8 +882,8 @@ __device__ __forceinline__ void chunk_pv_bf16(const uint8_t* slot, int lo, int h
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float sv = pscale(pw[e]);
-      wk[k_of_nib(e)] = mul_legacy(pv[e], sv * kPvScale);
-      cs += mul_legacy(pv[e], pzero(pw[e]) - kCodeBias * sv);
+      wk[k_of_nib(e)] = pv[e] * (sv * kPvScale);
+      cs = __builtin_fmaf(pv[e], pzero(pw[e]) - kCodeBias * sv, cs);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1017,9 +1075,8 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
     #pragma unroll
       for (int k = 0; k + 1 < D; ++k)
         if (k < nch) issue(k);
-      auto qk = [&](int c) {
+      auto qk = [&](int c, bool (&pok)[2]) {
         dma_wait<D>(min(D - 1, nch - 1 - c));
-        bool pok[2];
         split_page(spg, pi0 + 2 * c, &pok[0]);
         split_page(spg, pi0 + 2 * c + 1, &pok[1]);
         chunk_qk<R>(ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa, qk_scale, qs_lds,
@@ -1029,39 +1086,51 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
       // (pv_single_ok) and paired elsewhere, until one whose V scales fp16
       // cannot take; from that chunk on the piece finishes on bf16 pairs (a
       // second loop, so that each loop keeps its own register footprint).
+      // The chunk's V params, those of tokens outside the context zeroed.
+      auto load_vp = [&](int c, const bool (&pok)[2], u32x4& vp0, u32x4& vp1) {
+        read_chunk_vp(ring[c % D], lane, &vp0, &vp1);
+        if (!(pok[0] && pok[1] && tok_begin + 32 * c + 32 <= tok_end))
+          mask_vp_invalid(vp0, vp1, pok, tok_begin + 32 * c, tok_end, hi);
+      };
       int c = 0;
       bool pending = false;  // chunk c has had QK^T and the softmax, not PV
+      u32x4 pvp0, pvp1;      // and these V params
       for (; c < nch; ++c) {
         if (c + D - 1 < nch) issue(c + D - 1);
-        qk(c);
+        bool pok[2];
+        qk(c, pok);
         u32x4 vp0, vp1;
-        read_chunk_vp(ring[c % D], lane, &vp0, &vp1);
+        load_vp(c, pok, vp0, vp1);
         if (!pv_f16_range_ok(vp0, vp1)) {
           pending = true;
+          pvp0 = vp0;
+          pvp1 = vp1;
           break;
         }
         u32x4 a16[NT];
-        f16x2_t h16[NT][4];
-        float wx[NT], wr[NT];
-        pv_weights_f16<R>(vp0, vp1, lo, hi, p_lds, a16, h16, corr, wx, lsum);
-        // centered codes: take 8 x the weights the MFMA uses off the zero-point term
-        if (a.pv16 && pv_single_ok<R>(lo, h16, wsum, lsum, wr)) {
+        float wr[NT];
+        pv_weights_f16<R>(vp0, vp1, lo, hi, p_lds, a16, corr, lsum, wr);
+        // centered codes: 8 x the weights the MFMA takes come off the zero-point term
+        const bool single = a.pv16 && pv_single_ok<R>(lo, wr, wsum, lsum);
 #pragma unroll
-          for (int T = 0; T < NT; ++T) corr[T] = __builtin_fmaf(-8.0f, wr[T], corr[T]);
-          chunk_pv_f16<R>(ring[c % D], lane, a16, acc);
-        } else {
-#pragma unroll
-          for (int T = 0; T < NT; ++T) corr[T] = __builtin_fmaf(-8.0f, wx[T], corr[T]);
-          chunk_pv_f16_pair<R>(ring[c % D], lo, hi, p_lds, acc);
+        for (int T = 0; T < NT; ++T) corr[T] = __builtin_fmaf(-8.0f, wr[T], corr[T]);
+        chunk_pv_f16<R>(ring[c % D], lane, a16, acc);
+        if (!single) {
+          // the params again (their registers are not kept across the PV)
+          u32x4 wp0, wp1;
+          load_vp(c, pok, wp0, wp1);
+          chunk_pv_f16_lo<R>(ring[c % D], wp0, wp1, lo, hi, p_lds, corr, acc);
         }
       }
       for (; c < nch; ++c) {
         if (!pending) {
           if (c + D - 1 < nch) issue(c + D - 1);
-          qk(c);
+          bool pok[2];
+          qk(c, pok);
+          load_vp(c, pok, pvp0, pvp1);
         }
         pending = false;
-        chunk_pv_bf16<R>(ring[c % D], lo, hi, corr, acc, p_lds);
+        chunk_pv_bf16<R>(ring[c % D], pvp0, pvp1, lo, hi, corr, acc, p_lds);
       }
     }
 
