@@ -219,27 +219,19 @@ __device__ __forceinline__ float pzero(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
 }
 
-// h's high (fma_mix_hi, mul_mix_hi) or low (mul_mix_lo) fp16 half times x,
-// plus c (or +0), as one v_fma_mix_f32 (the fp16 operand converts exactly;
-// one rounding).  Written out because the compiler converts a param it uses
-// twice and then issues a separate fma for each use.  No operand may be an
-// MFMA result: the compiler does not insert the wait states such a result
-// needs before an inline-asm read.
-__device__ __forceinline__ float fma_mix_hi(uint32_t h, float x, float c) {
-  float r;
-  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-      : "=v"(r) : "v"(h), "v"(x), "v"(c));
-  return r;
+// One v_fma_mix_f32 with an fp16 operand taken from h's high or low half
+// (converted exactly; one rounding), in place: acc += hi(h) * x, or
+// x *= lo(h).  Written out because the compiler converts a param it uses
+// twice and then issues a separate fma for each use.  The result goes to the
+// register of a value the compiler has just written (acc's or x's): an
+// inline-asm write into a register that an MFMA still reads as its
+// accumulator input needs wait states the compiler inserts only for its own
+// instructions.  For the same reason no operand may be an MFMA result.
+__device__ __forceinline__ void fma_mix_hi_acc(float& acc, uint32_t h, float x) {
+  asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(h), "v"(x));
 }
-__device__ __forceinline__ float mul_mix_hi(uint32_t h, float x) {
-  float r;
-  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
-  return r;
-}
-__device__ __forceinline__ float mul_mix_lo(uint32_t h, float x) {
-  float r;
-  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
-  return r;
+__device__ __forceinline__ void mul_mix_lo_inplace(float& x, uint32_t h) {
+  asm("v_fma_mix_f32 %0, %1, %0, 0 op_sel_hi:[1,0,0]" : "+v"(x) : "v"(h));
 }
 
 // Query element as fp32 (bf16 or fp16 storage).
@@ -395,32 +387,54 @@ constexpr int kSlotBytes = 5120;
 // being read), which drains the ring each chunk.  dma_wait does the waiting
 // instead; loads the compiler issues complete in order with these DMAs, so
 // its own vmcnt waits stay valid (DMAs it does not count only make them
-// wait longer).  M0 holds the LDS address; one wait state separates its
-// write from the DMA.
-__device__ __forceinline__ void lds_dma16(const void* g, uint8_t* lds) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
-               : : "v"(g), "s"(m0) : "memory", "m0");
+// wait longer).  Each DMA takes a wave-uniform base in SGPRs and the lane's
+// 32-bit byte offset (the saddr form), so a chunk's addresses cost no VALU
+// work; lane i's bytes land at LDS address m0 + 16 i (dwordx4) or + 4 i
+// (dword).  One wait state separates the M0 write from the DMA.
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+               : : "v"(off), "s"(base), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void* base, uint32_t off, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1 nt"
+               : : "v"(off), "s"(base), "s"(m0) : "memory", "m0");
 }
 
-__device__ __forceinline__ void dma_chunk(const DecodeArgs& a, int64_t pg0, int64_t pg1, int h,
-                                          int lane, uint8_t* slot) {
+// LDS address of a __shared__ byte (wave-uniform for the ring slots).
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)p;
+}
+
+// The lane's byte offsets into a chunk's blocks, fixed for the kernel.
+struct DmaLane {
+  uint32_t koff;  // K codes: compute lane (t = lo, j = hi) reads slot lane,
+                  // bytes 64 t + 16 j .. + 15 of the (page, head) block
+  uint32_t voff;  // V codes: compute lane (lo, hi) needs the 32 bytes
+                  // 64 lo + 32 (hi & 1) of page hi >> 1, as halves j = 0, 1
+                  // in slots lo + 16 (hi & 1) + 32 j of that page
+  uint32_t poff;  // params: 4 bytes per lane of a 256-byte block
+};
+__device__ __forceinline__ DmaLane dma_lane(int lane) {
   const int lo = lane & 15, hi = lane >> 4;
+  return DmaLane{(uint32_t)(lo * 64 + hi * 16), (uint32_t)(64 * lo + 32 * (hi & 1) + 16 * (hi >> 1)),
+                 (uint32_t)(lane * 4)};
+}
+
+// The 8 DMAs of one chunk (pages pg0, pg1 of KV head h) into the slot at LDS
+// address m0: K codes of both pages, V codes of both pages, then the four
+// 256-byte param blocks (K0, K1, V0, V1) as they are.
+constexpr int kDmasPerChunk = 8;
+__device__ __forceinline__ void dma_chunk(const DecodeArgs& a, int64_t pg0, int64_t pg1, int h,
+                                          const DmaLane& dl, uint32_t m0) {
   const int64_t H = a.num_kv_heads, hb0 = pg0 * H + h, hb1 = pg1 * H + h;
-  // K: compute lane (t = lo, j = hi) reads slot lane; it needs code bytes
-  // 64 t + 16 j .. + 15 of the (page, head) block.
-  const int koff = lo * 64 + hi * 16;
-  // V: compute lane (lo, hi) needs the 32 bytes 64 lo + 32 (hi & 1) of page
-  // hi >> 1, as halves j = 0, 1 in slots lo + 16 (hi & 1) + 32 j of that page.
-  const int voff = 64 * lo + 32 * (hi & 1) + 16 * (hi >> 1);
-  lds_dma16(a.kc + hb0 * kHBCodes + koff, slot);
-  lds_dma16(a.kc + hb1 * kHBCodes + koff, slot + 1024);
-  lds_dma16(a.vc + hb0 * kHBCodes + voff, slot + 2048);
-  lds_dma16(a.vc + hb1 * kHBCodes + voff, slot + 3072);
-  // params: lanes 16 q .. 16 q + 15 copy block q = (K0, K1, V0, V1) as is.
-  const uint32_t* pb = (hi >> 1) ? a.vp : a.kp;
-  lds_dma16(pb + ((hi & 1) ? hb1 : hb0) * kHBParams + lo * 4, slot + 4096);
+  lds_dma16(a.kc + hb0 * kHBCodes, dl.koff, m0);
+  lds_dma16(a.kc + hb1 * kHBCodes, dl.koff, m0 + 1024);
+  lds_dma16(a.vc + hb0 * kHBCodes, dl.voff, m0 + 2048);
+  lds_dma16(a.vc + hb1 * kHBCodes, dl.voff, m0 + 3072);
+  lds_dma4(a.kp + hb0 * kHBParams, dl.poff, m0 + 4096);
+  lds_dma4(a.kp + hb1 * kHBParams, dl.poff, m0 + 4096 + 256);
+  lds_dma4(a.vp + hb0 * kHBParams, dl.poff, m0 + 4096 + 512);
+  lds_dma4(a.vp + hb1 * kHBParams, dl.poff, m0 + 4096 + 768);
 }
 
 // Operands of one chunk from its slot, in the MFMA lane layout.  K: codes
@@ -460,17 +474,19 @@ __device__ __forceinline__ void read_chunk_vp(const uint8_t* slot, int lane, u32
 template <int D>
 __device__ __forceinline__ void dma_wait(int newer) {
   static_assert(D >= 2 && D <= 4, "ring depth");
-  if (D >= 4 && newer >= 3) asm volatile("s_waitcnt vmcnt(15)" ::: "memory");
-  else if (D >= 3 && newer >= 2) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
-  else if (newer >= 1) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+  static_assert(kDmasPerChunk == 8, "the counts below are 8 per chunk");
+  if (D >= 4 && newer >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else if (D >= 3 && newer >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (newer >= 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Block-table entries of a split (at most 64 pages: split_tokens <= 1024),
 // one per lane; chunk code reads them back with readlane (wave-uniform).
 struct SplitPages {
-  int v;      // this lane's physical page id (or -1)
-  int first;  // logical page index of lane 0
+  int v;            // this lane's physical page id (or -1)
+  int first;        // logical page index of lane 0
+  uint64_t okmask;  // bit i: lane i's page is in the context with a valid id
 };
 
 // Lane's raw block-table entry of split sp, read before the context length
@@ -502,6 +518,7 @@ __device__ __forceinline__ SplitPages split_pages(const DecodeArgs& a, int raw, 
     }
   }
   sp.v = v;
+  sp.okmask = __ballot(v >= 0);
   return sp;
 }
 
@@ -567,14 +584,14 @@ __device__ __forceinline__ void chunk_qk(
       f32x4 cacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int st = 0; st < 4; ++st) cacc = mfma_f16(qa[T][st], kb[st], cacc);
-      // One fma chain: the zero-point terms (the zeros read as fp16 from the
-      // high halves of the param words), then the four scaled group sums
-      // (cacc, an MFMA result, is read by compiler-visible fmas only).
-      float sc = mul_mix_hi(kpar[u][0], qsum[0]);
+      // One fma chain: the four scaled group sums (cacc, an MFMA result, is
+      // read by compiler-visible operations only), then the zero-point terms
+      // (the zeros read as fp16 from the high halves of the param words).
+      float sc = ks[0] * cacc[0];
 #pragma unroll
-      for (int gi = 1; gi < 4; ++gi) sc = fma_mix_hi(kpar[u][gi], qsum[gi], sc);
+      for (int gi = 1; gi < 4; ++gi) sc = __builtin_fmaf(ks[gi], cacc[gi], sc);
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) sc = __builtin_fmaf(ks[gi], cacc[gi], sc);
+      for (int gi = 0; gi < 4; ++gi) fma_mix_hi_acc(sc, kpar[u][gi], qsum[gi]);
       x[T][u] = valid ? sc * qk_scale : -__builtin_inff();
     }
   }
@@ -739,8 +756,13 @@ __device__ __forceinline__ void pv_weights_f16(const u32x4& vp0, const u32x4& vp
     float cs = corr[T];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      w[e] = (e & 1) ? mul_mix_lo(pw[e], pv[e]) : pv[e] * s16[e];
       cs = __builtin_fmaf(pv[e], z8[e], cs);
+      if (e & 1) {
+        w[e] = pv[e];
+        mul_mix_lo_inplace(w[e], pw[e]);
+      } else {
+        w[e] = pv[e] * s16[e];
+      }
     }
     f16x2_t h16[4];
 #pragma unroll
@@ -930,6 +952,8 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
   const int H = a.num_kv_heads;
   __shared__ __attribute__((aligned(16))) float p_lds[NT][2][4][16];
   __shared__ __attribute__((aligned(16))) uint8_t ring[D][kSlotBytes];
+  const uint32_t ring_m0 = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]));
+  const DmaLane dl = dma_lane(lane);
   __shared__ __attribute__((aligned(16))) float qs_lds[NT][4][4];  // query group sums
 
   // ---- this wave's share: units (sequence, KV head, 32-token chunk) in that
@@ -1070,15 +1094,15 @@ void int4_decode_mfma_kernel(DecodeArgs a) {
         bool ok;
         const int64_t p0 = split_page(spg, pi0 + 2 * c, &ok);
         const int64_t p1 = split_page(spg, pi0 + 2 * c + 1, &ok);
-        dma_chunk(a, p0, p1, h, lane, ring[c % D]);
+        dma_chunk(a, p0, p1, h, dl, ring_m0 + (uint32_t)((c % D) * kSlotBytes));
       };
     #pragma unroll
       for (int k = 0; k + 1 < D; ++k)
         if (k < nch) issue(k);
       auto qk = [&](int c, bool (&pok)[2]) {
         dma_wait<D>(min(D - 1, nch - 1 - c));
-        split_page(spg, pi0 + 2 * c, &pok[0]);
-        split_page(spg, pi0 + 2 * c + 1, &pok[1]);
+        pok[0] = (spg.okmask >> (pi0 - spg.first + 2 * c)) & 1;
+        pok[1] = (spg.okmask >> (pi0 - spg.first + 2 * c + 1)) & 1;
         chunk_qk<R>(ring[c % D], pok, tok_begin + 32 * c, tok_end, lo, hi, qa, qk_scale, qs_lds,
                     m_run, l_run, corr, wsum, lsum, acc, p_lds);
       };
