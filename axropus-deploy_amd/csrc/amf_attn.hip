@@ -608,27 +608,382 @@ __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float*
   }
 }
 
-// One wave per query row: out = sum_k 2^(m_k - M) acc_k / sum_k 2^(m_k - M) l_k.
-// The split weights go through LDS; lane (phase, quad) then sums the f32x4
-// quad `quad` of the splits phase, phase + P, ... (P = 256 / D phases), with
-// the loads of four splits in flight, and the phases are added by shuffles.
+// ---- INT4_SYM split kernel on MFMA tiles (head_dim 128, bf16/fp16 q, no mask) ----
+//
+// The INT4_SYM scales are per channel, so they fold into the query and the
+// output: score = sum_d (q_d s_d) c_d - 8 sum_d q_d s_d and
+// out_d = s_d sum_t p_t (c_td - 8) / l, with c the raw codes.  The codes
+// enter v_mfma_f32_16x16x32_f16 as exact fp16 subnormals (c 2^-24; the high
+// nibble of a byte pair comes out x16 and its partner operand carries 1/16),
+// q s (exact in fp32: 8 or 11 by 11 bits) as an fp16 hi + lo pair that holds
+// it exactly after a per-wave power-of-two scaling, and p as an fp16 hi + lo
+// pair (22 bits).  The scores and PV sums are so exact products accumulated
+// in fp32: attention over the exactly dequantized K/V, where the codec's
+// restore rounds them to the cache dtype first.
+//
+// QK^T tile: rows = the wave's GH query heads (of 16; the rest zero), k = 32
+// dims, columns = 16 tokens.  Lane (token lo, slice hi) loads 16 bytes of its
+// token's code row, dims 32 hi .. 32 hi + 31, and word st of them is its B
+// operand of k-step st (dims 32 hi + 8 st + 0..7); the query operand follows
+// the same dim order.  PV needs tokens along k: an MFMA of the V codes (A:
+// row = token, k = the 32 dims of word m of every slice) against a constant
+// 0/1 selector (B: column c = one of 16 of those dims) transposes them, so
+// lane (dim c, r) receives tokens 4 r .. 4 r + 3 of the tile as exact fp32
+// (c - 8) 2^-24 (the -8 from the accumulator input), and the two 16-token
+// tiles of a chunk give the 8 tokens of its PV k-slice, converted back to
+// fp16 exactly.  Output dim of (word m, selector
+// half h, column c): 32 (2 h + c / 8) + 8 m + c % 8.
+constexpr float kNegBigAttn = -1.0e30f;
+constexpr float kRescaleSlackAttn = 8.0f;  // p <= 2^8 between rescales
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x4 mfma_f16(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pk_f16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((amf::f32x2){a, b}, f16x2_t));
+}
+
+// 8 nibbles of w as fp16 subnormals in the operand order
+// [n0 n4 n1 n5 n2 n6 n3 n7]: even nibbles c 2^-24, odd ones 16 c 2^-24.
+__host__ __device__ constexpr int nib_of_k16(int k) { return (k >> 1) + 4 * (k & 1); }
+__host__ __device__ constexpr bool k16_x16(int k) { return (k & 2) != 0; }
+__device__ __forceinline__ u32x4 nib8_to_f16_sub(uint32_t w) {
+  const uint32_t w8 = w >> 8;
+  return u32x4{w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u};
+}
+
+__device__ __forceinline__ float row_max16(float x) {
+  int v = __builtin_bit_cast(int, x);
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false)));
+  v = __builtin_bit_cast(int, x);
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false)));
+  v = __builtin_bit_cast(int, x);
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x122, 0xF, 0xF, false)));
+  v = __builtin_bit_cast(int, x);
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x121, 0xF, 0xF, false)));
+  return x;
+}
+
+template <int DT>
+__device__ __forceinline__ float qelem(uint32_t w, int half) {
+  const uint16_t b = (uint16_t)(half ? w >> 16 : w & 0xFFFFu);
+  if constexpr (DT == AMF_DTYPE_BF16) return amf::u2f((uint32_t)b << 16);
+  else return (float)__builtin_bit_cast(_Float16, b);
+}
+
+template <int DT, int GH>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+void int4_sym_attn_mfma_kernel(AttnArgs a, float* part,
+                                                                int64_t split_tokens,
+                                                                int64_t n_splits, int64_t units) {
+  constexpr int D = 128;
+  static_assert(GH >= 1 && GH <= 4, "heads per wave");
+  __shared__ __attribute__((aligned(16))) float p_lds[16][32];
+  const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
+  const int G = a.num_q_heads / a.num_kv_heads;
+  const int W = G / GH;
+  const int64_t id = blockIdx.x, slot = id / kXcds;
+  const int r = (int)(slot % W);
+  const int64_t u = (slot / W) * kXcds + id % kXcds;
+  if (u >= units) return;
+  const int64_t split = u % n_splits, rest = u / n_splits;
+  const int64_t tq = rest % a.q_len, bkv = rest / a.q_len;
+  const int hkv = (int)(bkv % a.num_kv_heads);
+  const int64_t b = bkv / a.num_kv_heads;
+  const int h0 = hkv * G + r * GH;
+  const int64_t T = a.kv_len;
+  const int64_t t_begin = split * split_tokens, t_end = min(T, t_begin + split_tokens);
+  const int64_t kv_base = (b * a.num_kv_heads + hkv) * T;
+  auto qrow = [&](int j) { return (b * a.num_q_heads + h0 + j) * a.q_len + tq; };
+  const float scl = a.scale * kLog2e;
+
+  // lane (lo, hi): 16 code bytes of token t0 + 16 j + lo, dims 32 hi .. + 31;
+  // the first chunk's are in flight while the query operand is built.  (The
+  // host keeps kv_len D / 2 below 2^32: 32-bit offsets from the row's base.)
+  const uint8_t* kcodes = static_cast<const uint8_t*>(a.k) + kv_base * (D / 2);
+  const uint8_t* vcodes = static_cast<const uint8_t*>(a.v) + kv_base * (D / 2);
+  auto row_off = [&](int64_t t) {
+    return (uint32_t)(t < t_end ? t : t_begin) * (uint32_t)(D / 2) + 16u * hi;
+  };
+  auto load = [&](u32x4 (&kx)[2], u32x4 (&vx)[2], int64_t t0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      kx[j] = *reinterpret_cast<const u32x4*>(kcodes + row_off(t0 + 16 * j + lo));
+      vx[j] = *reinterpret_cast<const u32x4*>(vcodes + row_off(t0 + 16 * j + lo));
+    }
+  };
+  u32x4 kc[2], vc[2];
+  load(kc, vc, t_begin);
+
+  // ---- query operand: x = q s over this lane's 32 dims (row lo) ----
+  // Rows GH .. 15 repeat row 0: they leave the maximum alone and their
+  // scores are masked below.
+  const int qr = lo < GH ? lo : 0;
+  float x[32];
+  {
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qrow(qr) * D + 32 * hi;
+    const uint16_t* sp = reinterpret_cast<const uint16_t*>(a.k_scales) + 32 * hi;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4 qw = *reinterpret_cast<const u32x4*>(qp + 8 * v);
+      const u32x4 sw = *reinterpret_cast<const u32x4*>(sp + 8 * v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float qv = qelem<DT>(qw[e >> 1], e & 1);
+        const float sv = qelem<AMF_DTYPE_F16>(sw[e >> 1], e & 1);
+        x[8 * v + e] = qv * sv;
+      }
+    }
+  }
+  float qsum = 0.0f, xmax = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 32; ++d) {
+    qsum += x[d];
+    xmax = fmaxf(xmax, fabsf(x[d]));
+  }
+  qsum += __shfl_xor(qsum, 16);
+  qsum += __shfl_xor(qsum, 32);
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) xmax = fmaxf(xmax, __shfl_xor(xmax, o));
+  // scale so that the largest |q s| lands in [2^14, 2^15): hi and lo then
+  // hold every q s above 2^-24 of it exactly
+  const int xexp = (int)((amf::f2u(xmax) >> 23) & 0xFFu);
+  const int qe = (xexp > 0 && xexp < 255) ? min(max(xexp - 127 - 14, -100), 100) : 0;
+  const float down = __builtin_ldexpf(1.0f, -qe);
+  u32x4 qa_hi[4], qa_lo[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      float v[2], h[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int i = 2 * jj + t;
+        v[t] = x[8 * st + nib_of_k16(i)] * (down * (k16_x16(i) ? 0.0625f : 1.0f));
+      }
+      const uint32_t hp = pk_f16(v[0], v[1]);
+      h[0] = amf::half_lo<false>(hp);
+      h[1] = amf::half_hi<false>(hp);
+      qa_hi[st][jj] = hp;
+      qa_lo[st][jj] = pk_f16(v[0] - h[0], v[1] - h[1]);
+    }
+  }
+  // scores: (MFMA sum) 2^(24 + qe) - 8 sum_d q_d s_d, times scale log2(e)
+  const float c1 = __builtin_ldexpf(scl, 24 + qe);
+  float c2[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) c2[e] = -8.0f * scl * __shfl(qsum, 4 * hi + e);
+
+  // ---- transpose selectors: column c takes dim 32 (2 h + c / 8) + 8 m + c % 8 ----
+  u32x4 sel[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      float v[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int i = 2 * jj + t;
+        const bool on = hi == 2 * h2 + (lo >> 3) && nib_of_k16(i) == (lo & 7);
+        v[t] = on ? (k16_x16(i) ? 0.0625f : 1.0f) : 0.0f;
+      }
+      sel[h2][jj] = pk_f16(v[0], v[1]);
+    }
+  }
+  float vsc[4][2];  // V scale of each output dim of this lane
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+      vsc[m][h2] = (float)a.v_scales[32 * (2 * h2 + (lo >> 3)) + 8 * m + (lo & 7)];
+
+  // the first chunk sets them: every split holds at least one token
+  float m_run[4], l_run[4];
+  f32x4 acc[4][2];
+
+  // One chunk on the codes in kc / vc, loading the next one into kn / vn.
+  // The first chunk of the split starts the running max, sums and
+  // accumulators.
+  auto chunk = [&](auto first_c, int64_t t0, u32x4 (&kn)[2], u32x4 (&vn)[2]) {
+    constexpr bool first = decltype(first_c)::value;
+    if (t0 + 32 < t_end) load(kn, vn, t0 + 32);
+    // QK^T: two 16-token tiles, hi and lo query parts against one code operand
+    float xs[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f32x4 cs = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const u32x4 kb = nib8_to_f16_sub(kc[j][st]);
+        cs = mfma_f16(qa_hi[st], kb, cs);
+        cs = mfma_f16(qa_lo[st], kb, cs);
+      }
+      const bool valid = t0 + 16 * j + lo < t_end;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xs[j][e] = (valid && 4 * hi + e < GH) ? fmaf(cs[e], c1, c2[e]) : -INFINITY;
+    }
+    // online softmax per head row (lanes of one 16-lane row share it): the
+    // reference max moves only when a score exceeds it by the slack
+    if constexpr (first) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        m_run[e] = fmaxf(kNegBigAttn, row_max16(fmaxf(xs[0][e], xs[1][e])));
+        l_run[e] = 0.0f;
+      }
+    } else {
+    bool up = false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) up = up || fmaxf(xs[0][e], xs[1][e]) > m_run[e] + kRescaleSlackAttn;
+    if (__any(up)) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float m_new = fmaxf(m_run[e], row_max16(fmaxf(xs[0][e], xs[1][e])));
+        const float alpha = __builtin_amdgcn_exp2f(m_run[e] - m_new);
+        l_run[e] *= alpha;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) acc[m][h2][e] *= alpha;
+        m_run[e] = m_new;
+      }
+    }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = __builtin_amdgcn_exp2f(xs[j][e] - m_run[e]);
+        l_run[e] += p;
+        p_lds[4 * hi + e][16 * j + lo] = p;
+      }
+    __builtin_amdgcn_wave_barrier();
+    // PV weights in the A layout: row lo, k-slice hi = tokens 4 hi .. + 3 and
+    // 16 + 4 hi .. + 3, as fp16 hi + lo
+    u32x4 pa_hi, pa_lo;
+    {
+      const f32x4 p0 = *reinterpret_cast<const f32x4*>(&p_lds[lo][4 * hi]);
+      const f32x4 p1 = *reinterpret_cast<const f32x4*>(&p_lds[lo][16 + 4 * hi]);
+      const float pv[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const uint32_t hp = pk_f16(pv[2 * jj], pv[2 * jj + 1]);
+        pa_hi[jj] = hp;
+        pa_lo[jj] = pk_f16(pv[2 * jj] - amf::half_lo<false>(hp),
+                           pv[2 * jj + 1] - amf::half_hi<false>(hp));
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // V codes transposed by the selectors, then PV
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const u32x4 av0 = nib8_to_f16_sub(vc[0][m]), av1 = nib8_to_f16_sub(vc[1][m]);
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        // centred codes: the accumulator starts at -8 2^-24, so the PV sums
+        // take c - 8 (exact in fp16) and the output needs no - 8 l term,
+        // which would cancel most of an average over many tokens
+        const f32x4 z = {-0x1p-21f, -0x1p-21f, -0x1p-21f, -0x1p-21f};
+        const f32x4 t0v = mfma_f16(av0, sel[h2], z);
+        const f32x4 t1v = mfma_f16(av1, sel[h2], z);
+        const u32x4 bv = {pk_f16(t0v[0], t0v[1]), pk_f16(t0v[2], t0v[3]),
+                          pk_f16(t1v[0], t1v[1]), pk_f16(t1v[2], t1v[3])};
+        const f32x4 a0 = first ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[m][h2];
+        acc[m][h2] = mfma_f16(pa_hi, bv, a0);
+        acc[m][h2] = mfma_f16(pa_lo, bv, acc[m][h2]);
+      }
+    }
+  };
+  u32x4 kn[2], vn[2];
+  auto next = [&] {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      kc[j] = kn[j];
+      vc[j] = vn[j];
+    }
+  };
+  chunk(std::true_type{}, t_begin, kn, vn);
+  next();
+  for (int64_t t0 = t_begin + 32; t0 < t_end; t0 += 32) {
+    chunk(std::false_type{}, t0, kn, vn);
+    next();
+  }
+  // ---- the split's partials: o_d = s_d sum p (c - 8), m, l per head ----
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int head = 4 * hi + e;
+    const float l = group_sum<16>(l_run[e]);
+    if (head < GH) {
+      float* pr = part + (qrow(head) * n_splits + split) * (int64_t)(D + kPartPad);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+          pr[32 * (2 * h2 + (lo >> 3)) + 8 * m + (lo & 7)] = vsc[m][h2] * (acc[m][h2][e] * 0x1p24f);
+      if (lo == 0) {
+        pr[D] = m_run[e];
+        pr[D + 1] = l;
+      }
+    }
+  }
+}
+
+// One workgroup of kMergeWaves waves per query row:
+// out = sum_k 2^(m_k - M) acc_k / sum_k 2^(m_k - M) l_k.  Every wave finds M
+// and the denominator over all splits and puts the split weights in LDS;
+// wave w then sums the splits w, w + kMergeWaves, ..., lane (phase, quad)
+// taking the f32x4 quad `quad` of every P-th of them (P = 256 / D phases).
+// The accumulator loads of its first kMergeBatch splits per lane do not
+// depend on the weights and are issued first, in flight with the (m, l)
+// loads.  Phases are added by shuffles, waves through LDS.
 constexpr int kMaxSplits = 4096;
+constexpr int kMergeWaves = 4;
+constexpr int kMergeBatch = 16;  // accumulator loads per lane in flight
 static_assert(kSplitWaves <= kMaxSplits, "dense_splits gives at most kSplitWaves splits");
 
 template <int OUT_DT, int D>
-__global__ __launch_bounds__(64) void dense_attn_merge_kernel(AttnArgs a, const float* part,
-                                                              int64_t n_splits) {
-  constexpr int Q = D / 4, P = 64 / Q, STRIDE = D + kPartPad;
+__global__ __launch_bounds__(64 * kMergeWaves) void dense_attn_merge_kernel(AttnArgs a,
+                                                                          const float* part,
+                                                                          int64_t n_splits) {
+  constexpr int Q = D / 4, P = 64 / Q, STRIDE = D + kPartPad, S = P * kMergeWaves;
   __shared__ float f_s[kMaxSplits];
-  const int lane = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) float o_s[kMergeWaves][D];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row = blockIdx.x;
   const int ns = (int)n_splits;
   const float* pr = part + row * n_splits * (int64_t)STRIDE;
-  float M = -INFINITY;
-  for (int k = lane; k < ns; k += 64) M = fmaxf(M, pr[(int64_t)k * STRIDE + D]);
+  const int quad = lane % Q, phase = lane / Q;
+  const int k0 = wv * P + phase;  // this lane's splits: k0, k0 + S, ...
+  f32x4 x[kMergeBatch];
+#pragma unroll
+  for (int i = 0; i < kMergeBatch; ++i) {
+    const int k = k0 + S * i;
+    x[i] = k < ns ? *reinterpret_cast<const f32x4*>(pr + (int64_t)k * STRIDE + 4 * quad)
+                  : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  // (m, l) of splits lane, lane + 64, ...: the first in registers
+  float m0 = -INFINITY, l0 = 0.0f;
+  if (lane < ns) {
+    const amf::f32x2 ml = *reinterpret_cast<const amf::f32x2*>(pr + (int64_t)lane * STRIDE + D);
+    m0 = ml[0];
+    l0 = ml[1];
+  }
+  float M = m0;
+  for (int k = lane + 64; k < ns; k += 64) M = fmaxf(M, pr[(int64_t)k * STRIDE + D]);
   for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  // every wave writes the same weights
   float den = 0.0f;
-  for (int k = lane; k < ns; k += 64) {
+  if (lane < ns) {
+    const float f = (M == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2f(m0 - M);
+    den = l0 * f;
+    f_s[lane] = f;
+  }
+  for (int k = lane + 64; k < ns; k += 64) {
     const float mk = pr[(int64_t)k * STRIDE + D];
     const float f = (M == -INFINITY || mk == -INFINITY) ? 0.0f : exp2f(mk - M);
     den = fmaf(pr[(int64_t)k * STRIDE + D + 1], f, den);
@@ -636,36 +991,38 @@ __global__ __launch_bounds__(64) void dense_attn_merge_kernel(AttnArgs a, const 
   }
   for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
   __syncthreads();
-  const int quad = lane % Q, phase = lane / Q;
   f32x4 o4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  int k = phase;
-  for (; k + 3 * P < ns; k += 4 * P) {
-    f32x4 x[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      x[u] = *reinterpret_cast<const f32x4*>(pr + (int64_t)(k + u * P) * STRIDE + 4 * quad);
+  for (int i = 0; i < kMergeBatch; ++i) {
+    const int k = k0 + S * i;
+    const float f = k < ns ? f_s[k] : 0.0f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float f = f_s[k + u * P];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o4[e] = fmaf(x[u][e], f, o4[e]);
-    }
+    for (int e = 0; e < 4; ++e) o4[e] = fmaf(x[i][e], f, o4[e]);
   }
-  for (; k < ns; k += P) {
-    const f32x4 x = *reinterpret_cast<const f32x4*>(pr + (int64_t)k * STRIDE + 4 * quad);
+  for (int k = k0 + S * kMergeBatch; k < ns; k += S) {
+    const f32x4 y = *reinterpret_cast<const f32x4*>(pr + (int64_t)k * STRIDE + 4 * quad);
     const float f = f_s[k];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o4[e] = fmaf(x[e], f, o4[e]);
+    for (int e = 0; e < 4; ++e) o4[e] = fmaf(y[e], f, o4[e]);
   }
 #pragma unroll
   for (int o = Q; o < 64; o <<= 1) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) o4[e] += __shfl_xor(o4[e], o);
   }
+  if (phase == 0) *reinterpret_cast<f32x4*>(&o_s[wv][4 * quad]) = o4;
+  __syncthreads();
   // a row whose scores are all -inf: 0 / 0 = NaN, as softmax gives
-  if (phase == 0) {
+  if (wv == 0 && phase == 0) {
+    f32x4 t = *reinterpret_cast<const f32x4*>(&o_s[0][4 * quad]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) store_out<OUT_DT>(a.out, row * D + 4 * quad + e, o4[e] / den);
+    for (int w = 1; w < kMergeWaves; ++w) {
+      const f32x4 u = *reinterpret_cast<const f32x4*>(&o_s[w][4 * quad]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] += u[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_out<OUT_DT>(a.out, row * D + 4 * quad + e, t[e] / den);
   }
 }
 
@@ -692,6 +1049,26 @@ void launch_split_gh(const AttnArgs& a, float* part, int64_t split_tokens, int64
         <<<grid, 64, 0, st>>>(a, part, split_tokens, n_splits, units);
 }
 
+void launch_merge(const AttnArgs& a, int32_t out_dtype, int64_t rows, const float* part,
+                  int64_t n_splits, hipStream_t st) {
+  const dim3 mgrid((unsigned)rows);
+#define AMF_MERGE(OUT)                                                                            \
+  if (a.head_dim == 64)                                                                           \
+    dense_attn_merge_kernel<OUT, 64><<<mgrid, 64 * kMergeWaves, 0, st>>>(a, part, n_splits);      \
+  else if (a.head_dim == 128)                                                                     \
+    dense_attn_merge_kernel<OUT, 128><<<mgrid, 64 * kMergeWaves, 0, st>>>(a, part, n_splits);     \
+  else                                                                                            \
+    dense_attn_merge_kernel<OUT, 256><<<mgrid, 64 * kMergeWaves, 0, st>>>(a, part, n_splits)
+  if (out_dtype == AMF_DTYPE_F32) {
+    AMF_MERGE(AMF_DTYPE_F32);
+  } else if (out_dtype == AMF_DTYPE_BF16) {
+    AMF_MERGE(AMF_DTYPE_BF16);
+  } else {
+    AMF_MERGE(AMF_DTYPE_F16);
+  }
+#undef AMF_MERGE
+}
+
 template <int DT, bool INT4>
 void launch_split(const AttnArgs& a, int32_t out_dtype, int64_t rows, float* part,
                   int64_t split_tokens, int64_t n_splits, hipStream_t st) {
@@ -704,22 +1081,25 @@ void launch_split(const AttnArgs& a, int32_t out_dtype, int64_t rows, float* par
     launch_split_gh<DT, INT4, 2>(a, part, split_tokens, n_splits, grid, units, st);
   else
     launch_split_gh<DT, INT4, 1>(a, part, split_tokens, n_splits, grid, units, st);
-  const dim3 mgrid((unsigned)rows);
-#define AMF_MERGE(OUT)                                                                   \
-  if (a.head_dim == 64)                                                                  \
-    dense_attn_merge_kernel<OUT, 64><<<mgrid, 64, 0, st>>>(a, part, n_splits);           \
-  else if (a.head_dim == 128)                                                            \
-    dense_attn_merge_kernel<OUT, 128><<<mgrid, 64, 0, st>>>(a, part, n_splits);          \
-  else                                                                                   \
-    dense_attn_merge_kernel<OUT, 256><<<mgrid, 64, 0, st>>>(a, part, n_splits)
-  if (out_dtype == AMF_DTYPE_F32) {
-    AMF_MERGE(AMF_DTYPE_F32);
-  } else if (out_dtype == AMF_DTYPE_BF16) {
-    AMF_MERGE(AMF_DTYPE_BF16);
-  } else {
-    AMF_MERGE(AMF_DTYPE_F16);
-  }
-#undef AMF_MERGE
+  launch_merge(a, out_dtype, rows, part, n_splits, st);
+}
+
+// The INT4_SYM split on MFMA tiles (head_dim 128, bf16 / fp16 queries, no
+// mask), with the same splits, partials and merge as launch_split.
+template <int DT>
+void launch_int4_mfma(const AttnArgs& a, int32_t out_dtype, int64_t rows, float* part,
+                      int64_t split_tokens, int64_t n_splits, hipStream_t st) {
+  int64_t units = 0;
+  const dim3 grid((unsigned)split_grid(rows, n_splits, a.num_q_heads, a.num_kv_heads, &units));
+  const dim3 block(64);
+  const int gh = heads_per_wave(a.num_q_heads, a.num_kv_heads);
+  if (gh == 4)
+    int4_sym_attn_mfma_kernel<DT, 4><<<grid, block, 0, st>>>(a, part, split_tokens, n_splits, units);
+  else if (gh == 2)
+    int4_sym_attn_mfma_kernel<DT, 2><<<grid, block, 0, st>>>(a, part, split_tokens, n_splits, units);
+  else
+    int4_sym_attn_mfma_kernel<DT, 1><<<grid, block, 0, st>>>(a, part, split_tokens, n_splits, units);
+  launch_merge(a, out_dtype, rows, part, n_splits, st);
 }
 
 template <int DT, int OUT_DT>
@@ -883,7 +1263,14 @@ extern "C" int amf_int4_sym_dense_attn(const void* q, int32_t dtype, const void*
   dense_splits(rows, heads_per_wave(num_q_heads, num_kv_heads), kv_len, &n_splits,
                &split_tokens);
   float* part = static_cast<float*>(workspace);
-  if (dtype == AMF_DTYPE_F32)
+  // the MFMA kernel addresses a (batch, KV head) row of codes with 32-bit offsets
+  const bool mfma = head_dim == 128 && !mask && dtype != AMF_DTYPE_F32 &&
+                    kv_len < ((int64_t)1 << 32) / 64;
+  if (mfma && dtype == AMF_DTYPE_BF16)
+    launch_int4_mfma<AMF_DTYPE_BF16>(a, out_dtype, rows, part, split_tokens, n_splits, st);
+  else if (mfma)
+    launch_int4_mfma<AMF_DTYPE_F16>(a, out_dtype, rows, part, split_tokens, n_splits, st);
+  else if (dtype == AMF_DTYPE_F32)
     launch_split<AMF_DTYPE_F32, true>(a, out_dtype, rows, part, split_tokens, n_splits, st);
   else if (dtype == AMF_DTYPE_BF16)
     launch_split<AMF_DTYPE_BF16, true>(a, out_dtype, rows, part, split_tokens, n_splits, st);

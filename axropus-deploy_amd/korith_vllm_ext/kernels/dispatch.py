@@ -189,8 +189,10 @@ def int4_sym_attention(q: torch.Tensor, k: Any, v: Any, scale: Optional[float],
                        mask: Optional[torch.Tensor], out_dtype: Optional[torch.dtype] = None
                        ) -> Optional[torch.Tensor]:
     """softmax(q k^T * scale + mask) v straight from int4_sym CompressedKV
-    K and V (amf_int4_sym_dense_attn): the same values decompress_to(q.dtype)
-    would restore, without writing them out.  None when k/v are not int4_sym
+    K and V (amf_int4_sym_dense_attn), without writing them out.  Head dim
+    128 with bf16/fp16 q and no mask attends over the exactly dequantized
+    values (code - 8) * scale on MFMA tiles; other shapes over the values
+    decompress_to(q.dtype) would restore.  None when k/v are not int4_sym
     CompressedKV of q's layout or the head dim is not 64/128/256 (the caller
     then restores and runs dense_attention)."""
     if q.dtype not in _DTYPES or q.dim() < 3 or q.shape[-1] not in _FUSED_HEAD_DIMS:

@@ -655,9 +655,10 @@ class PositionalDecodeCase:
     int4_sym CompressedKV (per-channel INT4, the dispatch key) of [batch,
     Hkv, tokens, D] bf16, q [batch, Hq, 1, D].  The reference materializes
     bf16 K/V and then runs matmul -> softmax -> matmul in bf16; here one
-    split-K kernel reads the codes in place and dequantizes each element to
-    the bf16 value the restore would write (amf_int4_sym_dense_attn), with a
-    merge launch after it."""
+    split-K kernel reads the codes in place (amf_int4_sym_dense_attn: MFMA
+    tiles on the raw codes, the per-channel scales folded into q and the
+    output, so it attends over the exactly dequantized values), with a merge
+    launch after it."""
 
     def __init__(self, batch=4, tokens=8192, q_heads=32, kv_heads=8, head_dim=128, seed=21):
         from korith_vllm_ext.codecs import get_codec
@@ -687,8 +688,9 @@ class PositionalDecodeCase:
         """The reference path on the host for sequence 0: decompress K and V
         (INT4PerChannelCodec.decompress_to restated), repeat the KV heads
         for the GQA group, then fallback_fp16_kernel's matmul -> softmax ->
-        matmul in bf16; the GPU output's distance from it and from float64
-        attention over the same dequantized K/V is reported."""
+        matmul in bf16; the distances of both outputs from float64 attention
+        over the exactly dequantized K/V ((c - 8) s), and from each other,
+        are reported."""
         from oracle import attention as oatt
         from oracle import codecs as oc
 
@@ -710,9 +712,9 @@ class PositionalDecodeCase:
 
         def timed() -> dict:
             t, runs, total = cpu_time(run, min_runs, min_seconds)
-            # float64 attention over the restored bf16 K/V, the values both paths consume
-            k32 = oc.int4_channel_decompress(kd, ks, shape, torch.bfloat16)[0].double().numpy()
-            v32 = oc.int4_channel_decompress(vd, vs, shape, torch.bfloat16)[0].double().numpy()
+            # float64 attention over the exact (c - 8) s (fp32 holds them exactly)
+            k32 = oc.int4_channel_decompress(kd, ks, shape, torch.float32)[0].double().numpy()
+            v32 = oc.int4_channel_decompress(vd, vs, shape, torch.float32)[0].double().numpy()
             qq = q[0, :, 0].double().numpy()
             f64 = np.empty((self.Hq, self.D))
             for h in range(self.Hq):

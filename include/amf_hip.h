@@ -370,12 +370,16 @@ int64_t amf_dense_attn_workspace_bytes(int64_t batch, int32_t num_q_heads,
  * and v_codes [batch, num_kv_heads, kv_len, head_dim / 2] packed codes
  * (element 2i in the low nibble of byte i), k_scales and v_scales the fp16
  * per-channel scales [head_dim], as an AMF_FMT_INT4_SYM codec leaves them.
- * Each element is dequantized as the codec's restore writes it into a cache
- * of dtype (q's dtype): (code - 8) * scale in fp32, rounded to dtype; the
- * result equals amf_dense_attn over the restored K/V to fp32 summation
- * order.  head_dim 64, 128 or 256; q 16-byte and codes 4-byte aligned; the
- * workspace of amf_dense_attn_workspace_bytes (AMF_ERR_WORKSPACE without
- * it).  kv_len 0 gives zeros.
+ * head_dim 128 with bf16 / fp16 q and no mask (the decode shape) runs on
+ * MFMA tiles with the scales folded into the query and the output: attention
+ * over the exactly dequantized K/V, (code - 8) * scale not rounded to dtype,
+ * with exact products accumulated in fp32 (softmax weights to 22 bits).
+ * Otherwise each element is dequantized as the codec's restore writes it
+ * into a cache of dtype (q's dtype): (code - 8) * scale in fp32, rounded to
+ * dtype, and the result equals amf_dense_attn over the restored K/V to fp32
+ * summation order.  head_dim 64, 128 or 256; q 16-byte and codes 4-byte
+ * aligned; the workspace of amf_dense_attn_workspace_bytes
+ * (AMF_ERR_WORKSPACE without it).  kv_len 0 gives zeros.
  * Replaces the decompress_to + fallback_fp16_kernel pair that
  * int4_decode_attention (int4_decode_attention.py:6-9 ->
  * kernels/dispatch.py:117-152) runs for "int4_sym" CompressedKV k/v. */
