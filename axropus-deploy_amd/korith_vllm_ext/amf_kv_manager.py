@@ -26,6 +26,7 @@ from __future__ import annotations
 
 import ctypes
 import logging
+import mmap
 import os
 import struct
 import threading
@@ -47,9 +48,12 @@ logger = logging.getLogger(__name__)
 # Snapshot files are read into the pinned staging buffer in chunks on a small
 # thread pool (positional reads release the GIL and share the file), so the
 # file side is not one single-threaded copy; KORITH_AMF_IO_THREADS sets the
-# pool size (1: one read call).  Writes stay one call: concurrent writes to
-# one file serialize in the kernel and measured slower (25 MB to /dev/shm:
-# 6.1-6.6 ms with 8 threads against 4.5-4.6 ms).
+# pool size (1: one read or write call).  Concurrent write() calls to one file
+# serialize on its inode lock and measured slower (25 MB to /dev/shm: 6.1-6.6
+# ms with 8 threads against 4.5-4.6 ms), so a save allocates the file
+# (posix_fallocate) on the pool while the pages are gathered and copied to the
+# host, maps it, and copies the blob in on the pool (page faults of a mapped
+# file run in parallel).
 _IO_CHUNK = 4 << 20
 _io_lock = threading.Lock()
 _io_pool: Optional[ThreadPoolExecutor] = None
@@ -91,6 +95,65 @@ def _read_file_into(fd: int, buf: memoryview, size: int) -> None:
         return
     for f in [_pool().submit(_pread_all, fd, buf, off, n) for off, n in _chunks(size)]:
         f.result()
+
+
+def _write_all(fd: int, data: memoryview) -> None:
+    done = 0
+    while done < len(data):
+        done += os.write(fd, data[done:])
+
+
+class _SnapshotFile:
+    """A snapshot file of a known size, created and allocated ahead of its
+    bytes (on the IO pool, while the device side runs), then filled through a
+    shared mapping by the pool; files where that fails are written by one
+    write() call instead."""
+
+    def __init__(self, path: Path, size: int):
+        self.path, self.size = path, size
+        self.fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+        self._ready = None
+        if _io_threads() > 1 and size >= 2 * _IO_CHUNK:
+            self._ready = _pool().submit(self._allocate)
+
+    def _allocate(self) -> Optional[mmap.mmap]:
+        try:
+            os.posix_fallocate(self.fd, 0, self.size)
+            return mmap.mmap(self.fd, self.size, flags=mmap.MAP_SHARED,
+                             prot=mmap.PROT_READ | mmap.PROT_WRITE)
+        except (OSError, ValueError):
+            return None
+
+    def write(self, blob: memoryview) -> None:
+        mm = self._ready.result() if self._ready is not None else None
+        if mm is None or len(blob) != self.size:
+            if mm is not None:
+                mm.close()
+            os.ftruncate(self.fd, 0)
+            os.lseek(self.fd, 0, os.SEEK_SET)
+            _write_all(self.fd, blob)
+            return
+        try:
+            dst = ctypes.addressof(ctypes.c_char.from_buffer(mm))
+            src = int(np.frombuffer(blob, dtype=np.uint8).ctypes.data)
+            # ctypes.memmove releases the GIL: one page-aligned piece per pool
+            # thread, copied in parallel
+            step = -(-self.size // _io_threads())
+            step = -(-step // mmap.PAGESIZE) * mmap.PAGESIZE
+            for f in [_pool().submit(ctypes.memmove, dst + off, src + off,
+                                     min(step, self.size - off))
+                      for off in range(0, self.size, step)]:
+                f.result()
+            del dst
+        finally:
+            mm.close()
+
+    def close(self) -> None:
+        if self._ready is not None and not self._ready.done():
+            mm = self._ready.result()
+            if mm is not None:
+                mm.close()
+        os.close(self.fd)
 
 
 
@@ -276,21 +339,35 @@ class AmfKvManager:
         k0 = _kv_planes(gpu_cache[0])[0]
         staging = self._device_staging(view.device, 2 * n_layers * n_blocks * page_bytes,
                                        page_bytes)
-        blob = self._direct_ctx().save_pages(
-            view, _paged._device_ids(ids, view.device), n_blocks, staging,
-            tokens=prompt_tokens,
-            n_kv_heads=int(k0.shape[-3]),  # the reference's shape[-3] of the page stack
-            head_dim=int(k0.shape[-1]), dtype_tag=_DTYPE_TAG.get(view.dtype, 0),
-            model_hash=key["model_hash"])
+        # the blob: header, layer table, then K and V pages of each layer with KV
+        kv_layers = sum(1 for l in range(view.n_layers) if view.planes[2 * l])
+        size = (_HEADER_SIZE + _LAYER_SIZE * view.n_layers
+                + 2 * kv_layers * n_blocks * page_bytes)
         tmp_path = kv_path.with_suffix(".kv.tmp")
         try:
-            with open(tmp_path, "wb") as f:
-                f.write(blob)
+            out = _SnapshotFile(tmp_path, size)
+        except OSError as exc:
+            logger.warning("[AMF_VLLM] save: cannot create %s: %s", tmp_path, exc)
+            return False
+        try:
+            try:
+                blob = self._direct_ctx().save_pages(
+                    view, _paged._device_ids(ids, view.device), n_blocks, staging,
+                    tokens=prompt_tokens,
+                    n_kv_heads=int(k0.shape[-3]),  # the reference's shape[-3] of the page stack
+                    head_dim=int(k0.shape[-1]), dtype_tag=_DTYPE_TAG.get(view.dtype, 0),
+                    model_hash=key["model_hash"])
+                out.write(blob)
+            finally:
+                out.close()
             os.replace(tmp_path, kv_path)
         except OSError as exc:
             logger.warning("[AMF_VLLM] save: write failed: %s", exc)
             tmp_path.unlink(missing_ok=True)
             return False
+        except BaseException:
+            tmp_path.unlink(missing_ok=True)
+            raise
         try:
             toks = np.asarray([int(t) for t in prompt_tokens], dtype="<i4")
             self._tok_filename(key).write_bytes(toks.tobytes())

@@ -201,6 +201,56 @@ def test_int4_sym_fused_matches_restore_path(dtype, lead, Hq, Hkv, Tq, T, D, mas
     assert out.dtype == dtype and torch.equal(out, fused.to(dtype))
 
 
+@pytest.mark.parametrize("case", ["gqa8_ragged", "rising", "flat", "large_q", "one_token"])
+def test_int4_sym_mfma_edge_cases(case):
+    """The MFMA INT4-sym kernel (head_dim 128, no mask) against float64
+    attention over the exactly dequantized K/V on inputs that drive its
+    corners: GQA 8 (two waves per group) over ragged splits; scores rising
+    along the context (the running max moves inside splits, by more than
+    the rescale slack); near-uniform softmax over 6000 tokens (the centred V
+    sums); large fp16 queries (the per-wave power-of-two scaling of q s);
+    a one-token context."""
+    from korith_vllm_ext.codecs import get_codec
+    from korith_vllm_ext.kernels import int4_sym_attention
+
+    dtype, B, Hq, Hkv, T = torch.bfloat16, 2, 8, 2, 3000
+    q_mul, scale = 1.0, 0.25
+    if case == "gqa8_ragged":
+        B, Hq, Hkv, T = 3, 16, 2, 5000 + 17
+    elif case == "flat":
+        q_mul, T = 1e-3, 6000
+    elif case == "large_q":
+        dtype, q_mul = torch.float16, 30.0
+    elif case == "one_token":
+        T = 1
+    print(f"int4_sym mfma edge case {case}: B={B} Hq={Hq} Hkv={Hkv} T={T}", flush=True)
+    g = torch.Generator().manual_seed(len(case) * 131 + T)
+    q = (torch.randn(B, Hq, 1, 128, generator=g) * q_mul).to(dtype).to(DEV)
+    k = torch.randn(B, Hkv, T, 128, generator=g) * 2
+    if case == "rising":
+        k = k * (1.0 + torch.arange(T, dtype=torch.float32) / 64.0)[:, None]
+    v = torch.randn(B, Hkv, T, 128, generator=g)
+    v[..., 5] += 40.0  # an outlier channel: a large V scale
+    codec = get_codec("int4_sym")
+    ck, cv = codec.compress(k.to(dtype).to(DEV)), codec.compress(v.to(dtype).to(DEV))
+    out = int4_sym_attention(q, ck, cv, scale, None, torch.float32)
+    torch.cuda.synchronize()
+    kd = codec.decompress_to(ck, torch.float32)  # (c - 8) s, exact in fp32
+    vd = codec.decompress_to(cv, torch.float32)
+    ref = oatt.dense_attention_f64(_f64(q), _f64(kd), _f64(vd), scale)
+    err = np.abs(out.cpu().numpy() - ref)
+    vmax = float(np.abs(_f64(vd)).max())
+    kx = np.repeat(_f64(kd), Hq // Hkv, axis=1)
+    smax = float(np.abs(np.einsum("bhqd,bhtd->bhqt", _f64(q), kx)).max()) * scale / math.log(2)
+    print(f"max |diff| {err.max():.3e} (max |v| {vmax:.2f}, max |score| {smax:.1f} in log2 units)",
+          flush=True)
+    assert np.isfinite(out.cpu().numpy()).all()
+    # fp32 accumulation of the exact products, relative to the V range, plus
+    # the fp32 rounding of scores this large (an error of 2^-22 |score| in a
+    # score moves the weights by that much relative)
+    assert err.max() <= 3e-4 * max(1.0, vmax / 4.0) + 2.0 ** -22 * smax * vmax
+
+
 def test_int4_sym_fused_empty_context_and_declines():
     """kv_len 0 gives zeros, all -inf scores NaN; head dims outside
     64/128/256 (32 here) and other formats decline (None), so the caller restores and

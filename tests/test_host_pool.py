@@ -155,3 +155,38 @@ def test_snapshot_file_io_round_trip(tmp_path, monkeypatch, size, threads):
     assert np.array_equal(np.frombuffer(bytes(back[:size]), dtype=np.uint8), data)
     with open(path, "rb") as f, pytest.raises(OSError):
         m._read_file_into(f.fileno(), memoryview(bytearray(size + 100)), size + 100)
+
+
+@pytest.mark.parametrize("size", [1000, (8 << 20) + 12345, (21 << 20) + 7])
+@pytest.mark.parametrize("threads", ["1", "4"])
+@pytest.mark.parametrize("blob_delta", [0, -5, 4096])
+def test_snapshot_file_write(tmp_path, monkeypatch, size, threads, blob_delta):
+    """A save's file side: the file allocated at the expected size and filled
+    through a mapping by the pool, or, when the blob's size differs from the
+    expected one (or with one thread, or below two chunks), written by one
+    call; the file holds exactly the blob either way, also over an older,
+    longer file of the same name."""
+    from korith_vllm_ext import amf_kv_manager as m
+
+    monkeypatch.setenv("KORITH_AMF_IO_THREADS", threads)
+    n = size + blob_delta
+    blob = np.random.default_rng(size + n).integers(0, 256, n, dtype=np.uint8)
+    path = tmp_path / "snap.kv.tmp"
+    path.write_bytes(b"\x55" * (size + 8192))
+    out = m._SnapshotFile(path, size)
+    try:
+        out.write(memoryview(blob.tobytes()))
+    finally:
+        out.close()
+    assert np.array_equal(np.fromfile(path, dtype=np.uint8), blob)
+
+
+def test_snapshot_file_close_without_write(tmp_path, monkeypatch):
+    """A save that fails before its blob exists still closes the file and
+    its mapping."""
+    from korith_vllm_ext import amf_kv_manager as m
+
+    monkeypatch.setenv("KORITH_AMF_IO_THREADS", "4")
+    out = m._SnapshotFile(tmp_path / "snap.kv.tmp", 16 << 20)
+    out.close()
+    assert (tmp_path / "snap.kv.tmp").stat().st_size == 16 << 20
