@@ -600,7 +600,10 @@ class DecodeCase:
         KV heads for GQA, then matmul -> softmax -> matmul in bf16
         (kernels/dispatch.py:117-152).  Copies the pages and this GPU call's
         output rows to the host now; the returned callable times the CPU path
-        and reports its distance from the GPU output."""
+        and reports the distances of the GPU's bf16 output from it and from
+        float64 attention over the fp32-dequantized K/V, of the same call with
+        fp32 output from float64 (no output rounding), and of the CPU path
+        from float64."""
         from oracle import attention as oatt
         from oracle import codecs as oc
 
@@ -608,6 +611,10 @@ class DecodeCase:
         D, H, R = self.D, self.kv_heads, self.q_heads // self.kv_heads
         torch.cuda.synchronize()
         gpu_out = self.out[:sample_seqs].float().cpu()
+        out32 = torch.empty(self.batch, self.q_heads, D, dtype=torch.float32, device=DEV)
+        self.launch(amf_hip_module().DECODE_MFMA, out32)
+        gpu32 = out32[:sample_seqs].cpu()
+        del out32
         q = self.q[:sample_seqs].cpu()
         seqs = []
         cpp = lay.code_bytes_per_page
@@ -636,15 +643,34 @@ class DecodeCase:
                 v = v.repeat_interleave(R, dim=0)[None].contiguous()
                 out[b] = oatt.fallback_attention(q[b][None, :, None, :], k, v)[0, :, 0]
 
+        def f64_reference() -> torch.Tensor:
+            ref = np.empty((sample_seqs, self.q_heads, D))
+            for b, (ctx, n, codes, params) in enumerate(seqs):
+                kv = oc.int4_asym_decompress(codes, params, 16, H, D, torch.float32)
+                qq = q[b].double().numpy()
+                for h in range(H):
+                    k = kv[0].reshape(n * 16, H, D)[:ctx, h].double().numpy()
+                    v = kv[1].reshape(n * 16, H, D)[:ctx, h].double().numpy()
+                    sc = k @ qq[h * R:(h + 1) * R].T / math.sqrt(D)
+                    p_ = np.exp(sc - sc.max(axis=0))
+                    ref[b, h * R:(h + 1) * R] = (p_ / p_.sum(axis=0)).T @ v
+            return torch.from_numpy(ref)
+
+        def rounded(err: dict) -> dict:
+            return {k: float(f"{v:.3e}") for k, v in err.items()}
+
         def timed() -> dict:
             t, runs, total = cpu_time(run, min_runs, min_seconds)
-            err = attn_errors(gpu_out, out.float())
+            f64 = f64_reference()
             return {"kv_tok_per_s": round(sum_ctx / t, 1),
                     "GB/s": round(1280 * H // 8 * sum_ctx / t / 1e9, 3),
                     "queries_per_s_per_layer": round(sample_seqs / t, 3), "seconds": round(t, 4),
                     "sample": f"{sample_seqs} of {batch} sequences ({sum_ctx} context "
                               f"tokens), median of {runs} runs ({total:.1f} s)",
-                    "gpu_vs_cpu_fallback": {k: float(f"{v:.3e}") for k, v in err.items()}}
+                    "gpu_vs_cpu_fallback": rounded(attn_errors(gpu_out, out.float())),
+                    "gpu_bf16_out_vs_f64": rounded(attn_errors(gpu_out, f64)),
+                    "gpu_f32_out_vs_f64": rounded(attn_errors(gpu32, f64)),
+                    "cpu_fallback_vs_f64": rounded(attn_errors(out.float(), f64))}
 
         return timed
 
@@ -688,9 +714,10 @@ class PositionalDecodeCase:
         """The reference path on the host for sequence 0: decompress K and V
         (INT4PerChannelCodec.decompress_to restated), repeat the KV heads
         for the GQA group, then fallback_fp16_kernel's matmul -> softmax ->
-        matmul in bf16; the distances of both outputs from float64 attention
-        over the exactly dequantized K/V ((c - 8) s), and from each other,
-        are reported."""
+        matmul in bf16; the distances of both outputs (the GPU's as the
+        contract returns it, in bf16, and from the same call with fp32 output)
+        from float64 attention over the exactly dequantized K/V ((c - 8) s),
+        and from each other, are reported."""
         from oracle import attention as oatt
         from oracle import codecs as oc
 
@@ -701,6 +728,9 @@ class PositionalDecodeCase:
         vd, vs = self.vc.data.cpu(), self.vc.scales.cpu()
         q = self.q.cpu()
         gpu = self.out.float().cpu()
+        from korith_vllm_ext.kernels import int4_sym_attention
+
+        gpu32 = int4_sym_attention(self.q, self.kc, self.vc, None, None, torch.float32).cpu()
         res = {}
 
         def run():
@@ -728,7 +758,8 @@ class PositionalDecodeCase:
                     "sample": f"sequence 0 of {self.B} ({self.T} tokens), median of {runs} runs "
                               f"({total:.1f} s)",
                     "gpu_vs_cpu_fallback": attn_errors(gpu[0, :, 0], res["fb"][0, :, 0].float()),
-                    "gpu_vs_f64": attn_errors(gpu[0, :, 0], f64t),
+                    "gpu_bf16_out_vs_f64": attn_errors(gpu[0, :, 0], f64t),
+                    "gpu_f32_out_vs_f64": attn_errors(gpu32[0, :, 0], f64t),
                     "cpu_fallback_vs_f64": attn_errors(res["fb"][0, :, 0].float(), f64t)}
 
         return timed
