@@ -20,7 +20,10 @@
 // PV product accumulates 8 dims per lane and head.  Each split leaves (max,
 // sum, acc[D]) per head in the workspace and a merge kernel combines a row's
 // splits with an LSE rescale.  The waves of one KV head's group run on one
-// XCD, so what they share is read from HBM about once.
+// XCD, so what they share is read from HBM about once.  INT4_SYM K/V at
+// head_dim 128 with bf16 / fp16 queries and no mask take an MFMA form of the
+// split kernel (int4_sym_attn_mfma_kernel, described where it is defined)
+// with the same splits, partials and merge.
 //
 // Single-pass path (other head dims, kv_len 0, or no workspace): one
 // workgroup (4 waves) per query row.  Wave w takes the 64-token chunks w,
