@@ -624,8 +624,8 @@ __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float*
 // in fp32: attention over the exactly dequantized K/V, where the codec's
 // restore rounds them to the cache dtype first.
 //
-// QK^T tile: rows = the wave's GH query heads (of 16; the rest zero), k = 32
-// dims, columns = 16 tokens.  Lane (token lo, slice hi) loads 16 bytes of its
+// QK^T tile: rows = the wave's GH query heads (of 16; the other rows repeat
+// row 0 and their scores are masked), k = 32 dims, columns = 16 tokens.  Lane (token lo, slice hi) loads 16 bytes of its
 // token's code row, dims 32 hi .. 32 hi + 31, and word st of them is its B
 // operand of k-step st (dims 32 hi + 8 st + 0..7); the query operand follows
 // the same dim order.  PV needs tokens along k: an MFMA of the V codes (A:
@@ -634,8 +634,8 @@ __global__ __launch_bounds__(64) void dense_attn_split_kernel(AttnArgs a, float*
 // lane (dim c, r) receives tokens 4 r .. 4 r + 3 of the tile as exact fp32
 // (c - 8) 2^-24 (the -8 from the accumulator input), and the two 16-token
 // tiles of a chunk give the 8 tokens of its PV k-slice, converted back to
-// fp16 exactly.  Output dim of (word m, selector
-// half h, column c): 32 (2 h + c / 8) + 8 m + c % 8.
+// fp16 exactly.  Output dim of (word m, selector half h, column c):
+// 32 (2 h + c / 8) + 8 m + c % 8.
 constexpr float kNegBigAttn = -1.0e30f;
 constexpr float kRescaleSlackAttn = 8.0f;  // p <= 2^8 between rescales
 
