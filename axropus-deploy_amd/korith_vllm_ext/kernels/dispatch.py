@@ -26,6 +26,7 @@ from __future__ import annotations
 import logging
 import math
 import os
+from collections import OrderedDict
 from typing import Any, Callable, Dict, Optional, Tuple
 
 import torch
@@ -104,6 +105,38 @@ def dispatch_kernel(storage_format: str, active_format: str) -> KernelFn:
 
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
+# Split-K scratch reused across calls: one buffer per (device, stream), grown
+# to the largest size asked for.  Calls on one stream run in order, so a
+# call's kernels start after the previous call's merge has read the buffer;
+# a stream under graph capture gets a buffer of its own per call instead.
+_SCRATCH: "OrderedDict[Tuple[int, int], torch.Tensor]" = OrderedDict()
+_SCRATCH_MAX = 16
+_SPLIT_WS: Dict[tuple, int] = {}  # (B, Hq, Hkv, Tq, T, D) -> workspace bytes
+
+
+def _scratch(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), stream)
+    buf = _SCRATCH.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _SCRATCH[key] = buf
+    _SCRATCH.move_to_end(key)
+    while len(_SCRATCH) > _SCRATCH_MAX:
+        _SCRATCH.popitem(last=False)
+    return buf
+
+
+def _split_workspace_bytes(B: int, Hq: int, Hkv: int, Tq: int, T: int, D: int) -> int:
+    key = (B, Hq, Hkv, Tq, T, D)
+    n = _SPLIT_WS.get(key)
+    if n is None:
+        if len(_SPLIT_WS) > 4096:
+            _SPLIT_WS.clear()
+        n = _SPLIT_WS[key] = int(amf_hip.load().amf_dense_attn_workspace_bytes(*key))
+    return n
+
 
 def _to_tensor(obj: Any, like: torch.Tensor) -> torch.Tensor:
     """A CompressedKV (decompressed on the GPU by its codec) or a tensor, in
@@ -150,13 +183,13 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Op
         mptr, ms = m4.data_ptr(), tuple(m4.stride())
     # split-K scratch (per-split softmax partials), 0 bytes when the shape
     # takes the single-pass kernel
-    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Hkv, Tq, T, D))
-    ws = torch.empty(wsb, dtype=torch.uint8, device=q.device) if wsb else None
+    wsb = _split_workspace_bytes(B, Hq, Hkv, Tq, T, D)
+    stream = amf_hip.stream_handle(q.device)
+    ws = _scratch(q.device, stream, wsb) if wsb else None
     amf_hip.call("amf_dense_attn", qc.data_ptr(), k.data_ptr(), v.data_ptr(),
                  amf_hip.dtype_tag(q.dtype), mptr, ms[0], ms[1], ms[2], ms[3], out.data_ptr(),
                  amf_hip.dtype_tag(out.dtype), B, Hq, Hkv, Tq, T, D, float(scale),
-                 ws.data_ptr() if ws is not None else None, wsb,
-                 amf_hip.stream_handle(q.device))
+                 ws.data_ptr() if ws is not None else None, wsb, stream)
     return out
 
 
@@ -218,15 +251,16 @@ def int4_sym_attention(q: torch.Tensor, k: Any, v: Any, scale: Optional[float],
         m4 = mask.to(device=q.device, dtype=torch.float32).expand(*q.shape[:-3], Hq, Tq, T)
         m4 = m4.reshape(B, Hq, Tq, T)
         mptr, ms = m4.data_ptr(), tuple(m4.stride())
-    wsb = int(amf_hip.load().amf_dense_attn_workspace_bytes(B, Hq, Hkv, Tq, T, D))
+    wsb = _split_workspace_bytes(B, Hq, Hkv, Tq, T, D)
     if T > 0 and wsb == 0:
         return None  # beyond one split launch: the restoring path takes it
-    ws = torch.empty(wsb, dtype=torch.uint8, device=q.device) if wsb else None
+    stream = amf_hip.stream_handle(q.device)
+    ws = _scratch(q.device, stream, wsb) if wsb else None
     amf_hip.call("amf_int4_sym_dense_attn", qc.data_ptr(), amf_hip.dtype_tag(q.dtype),
                  ko[0].data_ptr(), ko[1].data_ptr(), vo[0].data_ptr(), vo[1].data_ptr(), mptr,
                  ms[0], ms[1], ms[2], ms[3], out.data_ptr(), amf_hip.dtype_tag(out.dtype), B, Hq,
                  Hkv, Tq, T, D, float(scale), ws.data_ptr() if ws is not None else None, wsb,
-                 amf_hip.stream_handle(q.device))
+                 stream)
     return out
 
 
@@ -318,8 +352,9 @@ def paged_int4_decode(q: torch.Tensor, kv: CompressedKV, block_tables: torch.Ten
     wsb = amf_hip.decode_workspace_bytes(S, Hq, layout.num_heads, D, max_context_len)
     if workspace is not None:
         _check_buffer(workspace, "workspace", dev)
+    stream = amf_hip.stream_handle(dev)
     if workspace is None or workspace.numel() * workspace.element_size() < wsb:
-        workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=dev)
+        workspace = _scratch(dev, stream, max(wsb, 4))
     algos = {"auto": amf_hip.DECODE_AUTO, "valu": amf_hip.DECODE_VALU, "mfma": amf_hip.DECODE_MFMA,
              "mfma_precise": amf_hip.DECODE_MFMA_PRECISE}
     amf_hip.call(
@@ -329,8 +364,7 @@ def paged_int4_decode(q: torch.Tensor, kv: CompressedKV, block_tables: torch.Ten
         blob.data_ptr() + layout.param_offset(1), layout.n_pages, bt.data_ptr(), bt.shape[1],
         cl.data_ptr(), S, Hq, layout.num_heads, D, layout.block_size, int(max_context_len),
         float(scale) if scale else 0.0, workspace.data_ptr(),
-        workspace.numel() * workspace.element_size(), algos[algo], None,
-        amf_hip.stream_handle(dev))
+        workspace.numel() * workspace.element_size(), algos[algo], None, stream)
     return out.view(q.shape) if q.dim() == 4 else out
 
 
