@@ -378,3 +378,34 @@ def test_dispatch_resolves_to_hip_kernel():
     assert dispatch.get_current_sm_version() == dispatch.GFX950_VERSION
     assert dispatch.dispatch_kernel("int4_sym", "fp8_e4m3") is dispatch.hip_decode_attention
     assert dispatch.try_load_cuda_extension() is not None
+
+
+def test_int4_sym_attention_in_a_hip_graph():
+    """The positional INT4-sym call captured in a HIP graph (the split and
+    merge launches, the split scratch taken for the capture): every replay,
+    with eager calls of the same shape on the default stream in between,
+    gives the eager result bit for bit."""
+    from korith_vllm_ext.codecs import get_codec
+    from korith_vllm_ext.kernels import int4_sym_attention
+
+    g = torch.Generator().manual_seed(77)
+    q = torch.randn(2, 8, 1, 128, generator=g).to(torch.bfloat16).to(DEV)
+    codec = get_codec("int4_sym")
+    ck = codec.compress(torch.randn(2, 2, 1500, 128, generator=g).to(torch.bfloat16).to(DEV))
+    cv = codec.compress(torch.randn(2, 2, 1500, 128, generator=g).to(torch.bfloat16).to(DEV))
+    want = int4_sym_attention(q, ck, cv, None, None, torch.float32)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        int4_sym_attention(q, ck, cv, None, None, torch.float32)  # warm-up on the side stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = int4_sym_attention(q, ck, cv, None, None, torch.float32)
+    for _ in range(3):
+        got.zero_()
+        graph.replay()
+        eager = int4_sym_attention(q, ck, cv, None, None, torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+        assert torch.equal(eager, want)
