@@ -409,3 +409,42 @@ def test_int4_sym_attention_in_a_hip_graph():
         torch.cuda.synchronize()
         assert torch.equal(got, want)
         assert torch.equal(eager, want)
+
+
+def test_paged_decode_in_a_hip_graph():
+    """The paged INT4 decode (the decode launch and its merge) captured in a
+    HIP graph over caller-owned output and workspace: every replay, with an
+    eager call on other buffers in between, gives the eager result bit for
+    bit, and replays follow context lengths changed in place."""
+    import amf_hip
+    from korith_vllm_ext.codecs import get_codec
+    from korith_vllm_ext.int4_decode_attention import int4_decode_attention
+
+    g = torch.Generator().manual_seed(321)
+    Hkv, R, D, pool = 2, 4, 128, 64
+    pages = gen.kv_values((2, pool, 16, Hkv, D), D, g, True)
+    ckv = get_codec("int4_asym_g32").compress(pages.to(DEV))
+    ctx = torch.tensor([700, 37, 1000, 16], dtype=torch.int32, device=DEV)
+    bt = torch.stack([torch.randperm(pool, generator=g)[:63] for _ in range(4)]).to(torch.int32)
+    bt = bt.to(DEV)
+    q = torch.randn(4, Hkv * R, D, generator=g).to(torch.bfloat16).to(DEV)
+    wsb = amf_hip.decode_workspace_bytes(4, Hkv * R, Hkv, D, 63 * 16)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    out = torch.empty(4, Hkv * R, D, dtype=torch.float32, device=DEV)
+    kw = dict(block_tables=bt, context_lens=ctx, out=out, workspace=ws)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        int4_decode_attention(q, ckv, **kw)  # warm-up on the side stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        int4_decode_attention(q, ckv, **kw)
+    for lens in ([700, 37, 1000, 16], [5, 999, 1, 512], [700, 37, 1000, 16]):
+        ctx.copy_(torch.tensor(lens, dtype=torch.int32))
+        out.zero_()
+        graph.replay()
+        eager = int4_decode_attention(q, ckv, block_tables=bt, context_lens=ctx,
+                                      out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), lens
