@@ -910,10 +910,9 @@ void int4_sym_attn_mfma_kernel(AttnArgs a, float* part,
     }
   };
   chunk(std::true_type{}, t_begin, kn, vn);
-  next();
   for (int64_t t0 = t_begin + 32; t0 < t_end; t0 += 32) {
-    chunk(std::false_type{}, t0, kn, vn);
     next();
+    chunk(std::false_type{}, t0, kn, vn);
   }
   // ---- the split's partials: o_d = s_d sum p (c - 8), m, l per head ----
 #pragma unroll
@@ -937,7 +936,7 @@ void int4_sym_attn_mfma_kernel(AttnArgs a, float* part,
 
 // One workgroup of kMergeWaves waves per query row:
 // out = sum_k 2^(m_k - M) acc_k / sum_k 2^(m_k - M) l_k.  Every wave finds M
-// and the denominator over all splits and puts the split weights in LDS;
+// and the denominator over all splits, wave 0 puts the split weights in LDS;
 // wave w then sums the splits w, w + kMergeWaves, ..., lane (phase, quad)
 // taking the f32x4 quad `quad` of every P-th of them (P = 256 / D phases).
 // The accumulator loads of its first kMergeBatch splits per lane do not
@@ -979,18 +978,18 @@ __global__ __launch_bounds__(64 * kMergeWaves) void dense_attn_merge_kernel(Attn
   float M = m0;
   for (int k = lane + 64; k < ns; k += 64) M = fmaxf(M, pr[(int64_t)k * STRIDE + D]);
   for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-  // every wave writes the same weights
+  // every wave finds the denominator; wave 0 writes the weights
   float den = 0.0f;
   if (lane < ns) {
     const float f = (M == -INFINITY || m0 == -INFINITY) ? 0.0f : exp2f(m0 - M);
     den = l0 * f;
-    f_s[lane] = f;
+    if (wv == 0) f_s[lane] = f;
   }
   for (int k = lane + 64; k < ns; k += 64) {
     const float mk = pr[(int64_t)k * STRIDE + D];
     const float f = (M == -INFINITY || mk == -INFINITY) ? 0.0f : exp2f(mk - M);
     den = fmaf(pr[(int64_t)k * STRIDE + D + 1], f, den);
-    f_s[k] = f;
+    if (wv == 0) f_s[k] = f;
   }
   for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
   __syncthreads();
