@@ -482,3 +482,32 @@ def test_split_attention_many_splits(D, int4):
     # fp32 accumulation over 1e5 tokens (the MFMA kernel: of the raw-code
     # products, measured 9.1e-6); the other cases measured below 1e-7
     assert err <= (1e-4 if (int4 and D == 128) else 1e-5)
+
+
+def test_split_scratch_per_stream():
+    """The attention wrappers' split-K scratch is one buffer per (device,
+    stream): calls on two streams at once each use their own and both give
+    the single-stream result."""
+    from korith_vllm_ext.kernels import dense_attention
+    from korith_vllm_ext.kernels import dispatch
+
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(2, 8, 1, 128, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(2, 2, 3000, 128, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(2, 2, 3000, 128, generator=g).to(torch.bfloat16).to(DEV)
+    want = dense_attention(q, k, v, None, None, torch.float32)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    for s in (s1, s2):
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            outs.append([dense_attention(q, k, v, None, None, torch.float32) for _ in range(4)])
+    torch.cuda.synchronize()
+    for o in outs:
+        for x in o:
+            assert torch.equal(x, want)
+    idx = DEV.index if DEV.index is not None else torch.cuda.current_device()
+    bufs = {key: t.data_ptr() for key, t in dispatch._SCRATCH.items() if key[0] == idx}
+    assert (idx, s1.cuda_stream) in bufs and (idx, s2.cuda_stream) in bufs
+    assert bufs[(idx, s1.cuda_stream)] != bufs[(idx, s2.cuda_stream)]

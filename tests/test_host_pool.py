@@ -190,3 +190,24 @@ def test_snapshot_file_close_without_write(tmp_path, monkeypatch):
     out = m._SnapshotFile(tmp_path / "snap.kv.tmp", 16 << 20)
     out.close()
     assert (tmp_path / "snap.kv.tmp").stat().st_size == 16 << 20
+
+
+def test_snapshot_file_write_without_fallocate(tmp_path, monkeypatch):
+    """Where the file system cannot allocate ahead (posix_fallocate fails),
+    the save's file side falls back to one write of the whole blob."""
+    from korith_vllm_ext import amf_kv_manager as m
+
+    def refuse(fd, off, n):
+        raise OSError(95, "Operation not supported")
+
+    monkeypatch.setenv("KORITH_AMF_IO_THREADS", "4")
+    monkeypatch.setattr(m.os, "posix_fallocate", refuse)
+    size = (12 << 20) + 3
+    blob = np.random.default_rng(5).integers(0, 256, size, dtype=np.uint8)
+    path = tmp_path / "snap.kv.tmp"
+    out = m._SnapshotFile(path, size)
+    try:
+        out.write(memoryview(blob.tobytes()))
+    finally:
+        out.close()
+    assert np.array_equal(np.fromfile(path, dtype=np.uint8), blob)
