@@ -26,6 +26,7 @@ from __future__ import annotations
 import logging
 import math
 import os
+import threading
 from collections import OrderedDict
 from typing import Any, Callable, Dict, Optional, Tuple
 
@@ -111,6 +112,7 @@ _DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 # a stream under graph capture gets a buffer of its own per call instead.
 _SCRATCH: "OrderedDict[Tuple[int, int], torch.Tensor]" = OrderedDict()
 _SCRATCH_MAX = 16
+_SCRATCH_LOCK = threading.Lock()
 _SPLIT_WS: Dict[tuple, int] = {}  # (B, Hq, Hkv, Tq, T, D) -> workspace bytes
 
 
@@ -118,14 +120,15 @@ def _scratch(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     if torch.cuda.is_current_stream_capturing():
         return torch.empty(nbytes, dtype=torch.uint8, device=dev)
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), stream)
-    buf = _SCRATCH.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        _SCRATCH[key] = buf
-    _SCRATCH.move_to_end(key)
-    while len(_SCRATCH) > _SCRATCH_MAX:
-        _SCRATCH.popitem(last=False)
-    return buf
+    with _SCRATCH_LOCK:
+        buf = _SCRATCH.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            _SCRATCH[key] = buf
+        _SCRATCH.move_to_end(key)
+        while len(_SCRATCH) > _SCRATCH_MAX:
+            _SCRATCH.popitem(last=False)
+        return buf
 
 
 def _split_workspace_bytes(B: int, Hq: int, Hkv: int, Tq: int, T: int, D: int) -> int:
