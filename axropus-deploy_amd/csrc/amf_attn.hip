@@ -684,7 +684,7 @@ void int4_sym_attn_mfma_kernel(AttnArgs a, float* part,
                                                                 int64_t split_tokens,
                                                                 int64_t n_splits, int64_t units) {
   constexpr int D = 128;
-  static_assert(GH >= 1 && GH <= 4, "heads per wave");
+  static_assert(GH >= 1 && GH <= 16, "heads per wave: the 16 rows of the tile");
   __shared__ __attribute__((aligned(16))) float p_lds[16][32];
   const int lane = threadIdx.x, lo = lane & 15, hi = lane >> 4;
   const int G = a.num_q_heads / a.num_kv_heads;
@@ -1091,16 +1091,27 @@ void launch_split(const AttnArgs& a, int32_t out_dtype, int64_t rows, float* par
 template <int DT>
 void launch_int4_mfma(const AttnArgs& a, int32_t out_dtype, int64_t rows, float* part,
                       int64_t split_tokens, int64_t n_splits, hipStream_t st) {
-  int64_t units = 0;
-  const dim3 grid((unsigned)split_grid(rows, n_splits, a.num_q_heads, a.num_kv_heads, &units));
+  // Up to 16 heads of a GQA group per wave (the tile's rows), the largest
+  // power of two dividing the group: one wave reads a unit's codes for all
+  // of them.  The splits are those of the workspace (dense_splits).
+  const int G = a.num_q_heads / a.num_kv_heads;
+  const int gh = G % 16 == 0 ? 16 : G % 8 == 0 ? 8 : G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
+  const int64_t units = rows / G * n_splits;
+  const dim3 grid((unsigned)((units + kXcds - 1) / kXcds * kXcds * (G / gh)));
   const dim3 block(64);
-  const int gh = heads_per_wave(a.num_q_heads, a.num_kv_heads);
-  if (gh == 4)
-    int4_sym_attn_mfma_kernel<DT, 4><<<grid, block, 0, st>>>(a, part, split_tokens, n_splits, units);
+#define AMF_INT4_MFMA(GH) \
+  int4_sym_attn_mfma_kernel<DT, GH><<<grid, block, 0, st>>>(a, part, split_tokens, n_splits, units)
+  if (gh == 16)
+    AMF_INT4_MFMA(16);
+  else if (gh == 8)
+    AMF_INT4_MFMA(8);
+  else if (gh == 4)
+    AMF_INT4_MFMA(4);
   else if (gh == 2)
-    int4_sym_attn_mfma_kernel<DT, 2><<<grid, block, 0, st>>>(a, part, split_tokens, n_splits, units);
+    AMF_INT4_MFMA(2);
   else
-    int4_sym_attn_mfma_kernel<DT, 1><<<grid, block, 0, st>>>(a, part, split_tokens, n_splits, units);
+    AMF_INT4_MFMA(1);
+#undef AMF_INT4_MFMA
   launch_merge(a, out_dtype, rows, part, n_splits, st);
 }
 

@@ -201,11 +201,13 @@ def test_int4_sym_fused_matches_restore_path(dtype, lead, Hq, Hkv, Tq, T, D, mas
     assert out.dtype == dtype and torch.equal(out, fused.to(dtype))
 
 
-@pytest.mark.parametrize("case", ["gqa8_ragged", "rising", "flat", "large_q", "one_token"])
+@pytest.mark.parametrize("case", ["gqa8_ragged", "gqa16", "gqa12", "gqa6", "rising", "flat",
+                                  "large_q", "one_token"])
 def test_int4_sym_mfma_edge_cases(case):
     """The MFMA INT4-sym kernel (head_dim 128, no mask) against float64
     attention over the exactly dequantized K/V on inputs that drive its
-    corners: GQA 8 (two waves per group) over ragged splits; scores rising
+    corners: GQA 8 and 16 (one wave for the group) over ragged splits, GQA 12
+    and 6 (three waves of 4 and of 2 heads per group); scores rising
     along the context (the running max moves inside splits, by more than
     the rescale slack); near-uniform softmax over 6000 tokens (the centred V
     sums); large fp16 queries (the per-wave power-of-two scaling of q s);
@@ -217,6 +219,12 @@ def test_int4_sym_mfma_edge_cases(case):
     q_mul, scale = 1.0, 0.25
     if case == "gqa8_ragged":
         B, Hq, Hkv, T = 3, 16, 2, 5000 + 17
+    elif case == "gqa16":
+        B, Hq, Hkv, T = 2, 32, 2, 3000 + 5
+    elif case == "gqa12":
+        B, Hq, Hkv, T = 2, 24, 2, 2000
+    elif case == "gqa6":
+        B, Hq, Hkv, T = 2, 12, 2, 2000
     elif case == "flat":
         q_mul, T = 1e-3, 6000
     elif case == "large_q":
