@@ -107,8 +107,9 @@ def dispatch_kernel(storage_format: str, active_format: str) -> KernelFn:
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 # Split-K scratch reused across calls: one buffer per (device, stream), grown
-# to the largest size asked for.  Calls on one stream run in order, so a
-# call's kernels start after the previous call's merge has read the buffer;
+# to the largest size asked for, at most _SCRATCH_MAX of them (the one least
+# recently grown or added goes first).  Calls on one stream run in order, so
+# a call's kernels start after the previous call's merge has read the buffer;
 # a stream under graph capture gets a buffer of its own per call instead.
 _SCRATCH: "OrderedDict[Tuple[int, int], torch.Tensor]" = OrderedDict()
 _SCRATCH_MAX = 16
@@ -120,6 +121,9 @@ def _scratch(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     if torch.cuda.is_current_stream_capturing():
         return torch.empty(nbytes, dtype=torch.uint8, device=dev)
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), stream)
+    buf = _SCRATCH.get(key)
+    if buf is not None and buf.numel() >= nbytes:
+        return buf  # the common case: no reordering, no lock
     with _SCRATCH_LOCK:
         buf = _SCRATCH.get(key)
         if buf is None or buf.numel() < nbytes:
@@ -205,18 +209,22 @@ def _int4_sym_operands(c: Any, q: torch.Tensor) -> Optional[Tuple[torch.Tensor, 
     [D], both on q's device, lead dims equal to q's; None otherwise."""
     if not isinstance(c, CompressedKV) or c.format != FMT_INT4_SYM:
         return None
-    shape = tuple(int(d) for d in c.shape)
-    if len(shape) != q.dim() or shape[:-3] != tuple(q.shape[:-3]) or shape[-1] != q.shape[-1]:
+    shape = c.shape
+    if not isinstance(shape, tuple):
+        shape = tuple(int(d) for d in shape)
+    qs = q.shape
+    if len(shape) != len(qs) or shape[-1] != qs[-1] or shape[:-3] != qs[:-3]:
         return None
     D = shape[-1]
     codes, scales = c.data, c.scales
     if not isinstance(codes, torch.Tensor) or not isinstance(scales, torch.Tensor):
         return None
-    if (codes.dtype != torch.uint8 or tuple(codes.shape) != shape[:-1] + (D // 2,)
-            or not codes.is_contiguous() or codes.device != q.device):
+    dev = q.device
+    if (codes.dtype != torch.uint8 or codes.shape != shape[:-1] + (D // 2,)
+            or not codes.is_contiguous() or codes.device != dev):
         return None
     if (scales.dtype != torch.float16 or scales.numel() != D or not scales.is_contiguous()
-            or scales.device != q.device):
+            or scales.device != dev):
         return None
     return codes, scales
 
